@@ -1,0 +1,177 @@
+// Device-side building blocks shared by every switchyard kernel (gfx950 only).
+//
+// Data moves in 16-byte chunks: 8 bf16/fp16 values or 4 fp32 values, one
+// buffer_load_dwordx4 per lane. Each lane owns fixed chunks of a row; 64 lanes
+// of a wave read 1 KiB of contiguous row memory per instruction.
+//
+// All arithmetic is fp32. Sums of squares and query dot products of 16-bit
+// data use v_dot2_f32_{bf16,f16} (two exact products, fp32 accumulate), which
+// halves the VALU count of the reductions; fp32 data uses plain FMAs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sy {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// dtype tags. `code` matches sy_dtype in include/switchyard.h.
+struct BF16 { using storage = uint16_t; static constexpr int code = 2; static constexpr int ce = 8; };
+struct F16  { using storage = uint16_t; static constexpr int code = 1; static constexpr int ce = 8; };
+struct F32  { using storage = float;    static constexpr int code = 0; static constexpr int ce = 4; };
+
+// Buffer resource word 3 for gfx9-family raw buffers (32-bit dword format).
+constexpr int kRsrcFlags = 0x00020000;
+
+// A raw buffer over [p, p + bytes). Loads past `bytes` return 0 and stores
+// past it are dropped, which gives free masking of partial rows.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kRsrcFlags);
+}
+
+__device__ __forceinline__ i32x4_t ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+__device__ __forceinline__ void st16(__amdgpu_buffer_rsrc_t r, uint32_t off, i32x4_t x) {
+  __builtin_amdgcn_raw_buffer_store_b128(x, r, off, 0, 0);
+}
+
+// ---------------------------------------------------------------- conversion
+
+__device__ __forceinline__ float bf_lo(uint32_t x) { return __uint_as_float(x << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
+
+// Element e of a 16-byte chunk as fp32.
+template <class T> __device__ __forceinline__ float elem(const i32x4_t& c, int e);
+template <> __device__ __forceinline__ float elem<BF16>(const i32x4_t& c, int e) {
+  const uint32_t x = (uint32_t)c[e >> 1];
+  return (e & 1) ? bf_hi(x) : bf_lo(x);
+}
+template <> __device__ __forceinline__ float elem<F16>(const i32x4_t& c, int e) {
+  const int word = c[e >> 1];  // copy first: bit_cast of a vector element reads lane 0
+  const f16x2_t h = __builtin_bit_cast(f16x2_t, word);
+  return (e & 1) ? (float)h.y : (float)h.x;
+}
+template <> __device__ __forceinline__ float elem<F32>(const i32x4_t& c, int e) {
+  return __int_as_float(c[e]);
+}
+
+// Round fp32 values to the storage type (round-to-nearest-even) and pack.
+template <class T> __device__ __forceinline__ i32x4_t pack(const float* f);
+template <> __device__ __forceinline__ i32x4_t pack<BF16>(const float* f) {
+  i32x4_t r;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const f32x2_t p = {f[2 * k], f[2 * k + 1]};
+    r[k] = __builtin_bit_cast(int, __builtin_convertvector(p, bf16x2_t));
+  }
+  return r;
+}
+template <> __device__ __forceinline__ i32x4_t pack<F16>(const float* f) {
+  i32x4_t r;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const f32x2_t p = {f[2 * k], f[2 * k + 1]};
+    r[k] = __builtin_bit_cast(int, __builtin_convertvector(p, f16x2_t));
+  }
+  return r;
+}
+template <> __device__ __forceinline__ i32x4_t pack<F32>(const float* f) {
+  i32x4_t r;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) r[k] = __float_as_int(f[k]);
+  return r;
+}
+
+// acc + sum_e a[e] * b[e] over one chunk.
+template <class T> __device__ __forceinline__ float dot(const i32x4_t& a, const i32x4_t& b, float acc);
+template <> __device__ __forceinline__ float dot<BF16>(const i32x4_t& a, const i32x4_t& b, float acc) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    // Copy the dwords out first: __builtin_bit_cast applied directly to an
+    // ext_vector element reads element 0 whatever the index.
+    const int ak = a[k], bk = b[k];
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, ak),
+                                          __builtin_bit_cast(bf16x2_t, bk), acc, false);
+  }
+  return acc;
+}
+template <> __device__ __forceinline__ float dot<F16>(const i32x4_t& a, const i32x4_t& b, float acc) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int ak = a[k], bk = b[k];
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, ak), __builtin_bit_cast(f16x2_t, bk),
+                                 acc, false);
+  }
+  return acc;
+}
+template <> __device__ __forceinline__ float dot<F32>(const i32x4_t& a, const i32x4_t& b, float acc) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) acc = fmaf(__int_as_float(a[k]), __int_as_float(b[k]), acc);
+  return acc;
+}
+
+// Scalar element load/store for the generic (unaligned) path.
+__device__ __forceinline__ float load_elem(const void* p, int64_t i, int dtype) {
+  if (dtype == 2) return __uint_as_float((uint32_t)((const uint16_t*)p)[i] << 16);
+  if (dtype == 1) return (float)((const _Float16*)p)[i];
+  return ((const float*)p)[i];
+}
+__device__ __forceinline__ void store_elem(void* p, int64_t i, float x, int dtype) {
+  if (dtype == 2) {
+    ((__bf16*)p)[i] = (__bf16)x;
+  } else if (dtype == 1) {
+    ((_Float16*)p)[i] = (_Float16)x;
+  } else {
+    ((float*)p)[i] = x;
+  }
+}
+
+// ---------------------------------------------------------------- reductions
+
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xf, false));
+}
+
+// Sum over the 64 lanes of a wave, returned as a wave-uniform value. Six DPP
+// adds leave the total in lane 63 (quad swaps, half-row and row mirrors, then
+// the two row broadcasts), and one readlane makes it uniform. The order of the
+// adds is fixed, so every wave of a kernel rounds identically.
+__device__ __forceinline__ float wave_sum(float x) {
+  x += dpp<0xB1>(x);          // quad_perm [1,0,3,2]
+  x += dpp<0x4E>(x);          // quad_perm [2,3,0,1]
+  x += dpp<0x141>(x);         // row_half_mirror
+  x += dpp<0x140>(x);         // row_mirror: every lane holds its row's sum
+  x += dpp<0x142, 0xa>(x);    // row_bcast:15 into rows 1 and 3
+  x += dpp<0x143, 0xc>(x);    // row_bcast:31 into rows 2 and 3
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+
+// Max over the 64 lanes, wave-uniform. Rows that a broadcast skips see -inf
+// from the DPP `old` operand, which leaves the max unchanged.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_or_ninf(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp((int)0xff800000, __float_as_int(x), CTRL,
+                                                    ROW_MASK, 0xf, false));
+}
+__device__ __forceinline__ float wave_max(float x) {
+  x = fmaxf(x, dpp_or_ninf<0xB1>(x));
+  x = fmaxf(x, dpp_or_ninf<0x4E>(x));
+  x = fmaxf(x, dpp_or_ninf<0x141>(x));
+  x = fmaxf(x, dpp_or_ninf<0x140>(x));
+  x = fmaxf(x, dpp_or_ninf<0x142, 0xa>(x));
+  x = fmaxf(x, dpp_or_ninf<0x143, 0xc>(x));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+}
+
+}  // namespace sy

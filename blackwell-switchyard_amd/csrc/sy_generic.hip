@@ -1,0 +1,342 @@
+// Generic kernels for shapes the register-tiled kernels do not cover: rows
+// that are not 16-byte aligned (D = 777, D = 63, ...), a query whose dtype
+// differs from v's, N beyond the tile budgets, or very wide D. One 256-thread
+// workgroup per token, element-wise loads, two passes: the first computes the
+// per-row scalars (kept in LDS), the second re-reads v to produce outputs. The
+// second read is served from L2 for all but the widest rows. These are
+// correctness paths; the vector kernels carry the performance.
+//
+// Also here: the deterministic dw reduction that finishes every backward, and
+// the HBM probes (reference bench/machine.py:41-61).
+#include "sy_device.hpp"
+#include "sy_launch.hpp"
+
+namespace sy {
+
+namespace {
+
+constexpr int kBlock = 256;
+
+// Block-wide sum / max with a fixed combination order. `scr` holds >= 257
+// floats; callers must not reuse it until the next barrier.
+__device__ float block_sum(float x, float* scr) {
+  const int tid = threadIdx.x;
+  scr[tid] = x;
+  __syncthreads();
+  if (tid < 64) {
+    float s = ((scr[tid] + scr[tid + 64]) + scr[tid + 128]) + scr[tid + 192];
+    s = wave_sum(s);
+    if (tid == 0) scr[256] = s;
+  }
+  __syncthreads();
+  const float r = scr[256];
+  __syncthreads();
+  return r;
+}
+
+__device__ float block_max(float x, float* scr) {
+  const int tid = threadIdx.x;
+  scr[tid] = x;
+  __syncthreads();
+  if (tid < 64) {
+    float s = fmaxf(fmaxf(scr[tid], scr[tid + 64]), fmaxf(scr[tid + 128], scr[tid + 192]));
+    s = wave_max(s);
+    if (tid == 0) scr[256] = s;
+  }
+  __syncthreads();
+  const float r = scr[256];
+  __syncthreads();
+  return r;
+}
+
+// Pass 1 for one token: per-row (sum of squares, query dot[, grad dot]) for
+// every row, written to ss[], qd[] and gd[] in LDS. Rows go in groups of 8 so
+// a thread carries 16-24 partial sums.
+__device__ void row_scalars(const void* v, const void* w, const void* g, int n_src, int64_t tok,
+                            int d, int64_t src_stride, int vt, int wt, float* ss, float* qd,
+                            float* gd, float* scr) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  constexpr int R = 8;
+  for (int g0 = 0; g0 < n_src; g0 += R) {
+    float a[R], b[R], c[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) a[r] = b[r] = c[r] = 0.0f;
+    for (int k = tid; k < d; k += kBlock) {
+      const float wk = load_elem(w, k, wt);
+      const float gk = g ? load_elem(g, tok * d + k, vt) : 0.0f;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if (g0 + r < n_src) {
+          const float x = load_elem(v, (int64_t)(g0 + r) * src_stride + tok * d + k, vt);
+          a[r] = fmaf(x, x, a[r]);
+          b[r] = fmaf(x, wk, b[r]);
+          c[r] = fmaf(x, gk, c[r]);
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      a[r] = wave_sum(a[r]);
+      b[r] = wave_sum(b[r]);
+      c[r] = wave_sum(c[r]);
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        scr[wave * 3 * R + r] = a[r];
+        scr[wave * 3 * R + R + r] = b[r];
+        scr[wave * 3 * R + 2 * R + r] = c[r];
+      }
+    }
+    __syncthreads();
+    if (tid < R && g0 + tid < n_src) {
+      float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f;
+      for (int q = 0; q < kBlock / 64; ++q) {
+        s0 += scr[q * 3 * R + tid];
+        s1 += scr[q * 3 * R + R + tid];
+        s2 += scr[q * 3 * R + 2 * R + tid];
+      }
+      ss[g0 + tid] = s0;
+      qd[g0 + tid] = s1;
+      if (gd) gd[g0 + tid] = s2;
+    }
+    __syncthreads();
+  }
+}
+
+// LDS layout (floats): [0, n) lg, [n, 2n) ss/r, [2n, 3n) gd, then 257 scratch.
+__global__ void __launch_bounds__(kBlock)
+k_fwd_generic(const void* __restrict__ v, const void* __restrict__ w, void* __restrict__ out,
+              float* __restrict__ stats, int n_src, int64_t n_tok, int d, int64_t src_stride,
+              int vt, int wt, float eps, float inv_d) {
+  extern __shared__ float sh[];
+  float* lg = sh;
+  float* ss = sh + n_src;
+  float* scr = sh + 2 * n_src;
+  const int tid = threadIdx.x;
+  const int64_t tok = blockIdx.x;
+  row_scalars(v, w, nullptr, n_src, tok, d, src_stride, vt, wt, ss, lg, nullptr, scr);
+
+  float m = -INFINITY;
+  for (int n = tid; n < n_src; n += kBlock) {
+    const float r = rsqrtf(fmaf(ss[n], inv_d, eps));
+    lg[n] *= r;
+    ss[n] = r;
+    m = fmaxf(m, lg[n]);
+  }
+  m = block_max(m, scr);
+  float l = 0.0f;
+  for (int n = tid; n < n_src; n += kBlock) l += expf(lg[n] - m);
+  l = block_sum(l, scr);
+  const float inv_l = 1.0f / l;
+  if (stats) {
+    for (int n = tid; n < n_src; n += kBlock) {
+      stats[(int64_t)n * n_tok + tok] = lg[n];
+      stats[(int64_t)(n_src + n) * n_tok + tok] = ss[n];
+    }
+  }
+  __syncthreads();
+  for (int n = tid; n < n_src; n += kBlock) lg[n] = expf(lg[n] - m) * inv_l;
+  __syncthreads();
+  for (int k = tid; k < d; k += kBlock) {
+    float acc = 0.0f;
+    for (int n = 0; n < n_src; ++n)
+      acc = fmaf(lg[n], load_elem(v, (int64_t)n * src_stride + tok * d + k, vt), acc);
+    store_elem(out, tok * d + k, acc, vt);
+  }
+}
+
+__global__ void __launch_bounds__(kBlock)
+k_sol_generic(const void* __restrict__ v, void* __restrict__ out, int n_src, int64_t n_tok, int d,
+              int64_t src_stride, int vt) {
+  const int64_t tok = blockIdx.x;
+  for (int k = threadIdx.x; k < d; k += kBlock) {
+    float acc = 0.0f;
+    for (int n = 0; n < n_src; ++n) acc += load_elem(v, (int64_t)n * src_stride + tok * d + k, vt);
+    store_elem(out, tok * d + k, acc, vt);
+  }
+}
+
+// Persistent over tokens; workgroup b accumulates its dw contribution in its
+// own fp32 row partial[b][:] (no other workgroup touches it).
+__global__ void __launch_bounds__(kBlock)
+k_bwd_generic(const void* __restrict__ v, const void* __restrict__ w, const void* __restrict__ g,
+              void* __restrict__ dv, float* __restrict__ partial, int n_src, int64_t n_tok, int d,
+              int64_t src_stride, int vt, int wt, float eps, float inv_d) {
+  extern __shared__ float sh[];
+  float* al = sh;              // logit, then alpha
+  float* da = sh + n_src;      // sum of squares, then r, then da
+  float* gc = sh + 2 * n_src;  // grad dot, then c
+  float* scr = sh + 3 * n_src;
+  const int tid = threadIdx.x;
+  float* prow = partial + (int64_t)blockIdx.x * d;
+  for (int k = tid; k < d; k += kBlock) prow[k] = 0.0f;
+  const int64_t dv_stride = n_tok * d;
+
+  for (int64_t tok = blockIdx.x; tok < n_tok; tok += gridDim.x) {
+    row_scalars(v, w, g, n_src, tok, d, src_stride, vt, wt, da, al, gc, scr);
+    float m = -INFINITY;
+    for (int n = tid; n < n_src; n += kBlock) {
+      const float r = rsqrtf(fmaf(da[n], inv_d, eps));
+      al[n] *= r;
+      da[n] = r;
+      m = fmaxf(m, al[n]);
+    }
+    m = block_max(m, scr);
+    float l = 0.0f, sp = 0.0f;
+    for (int n = tid; n < n_src; n += kBlock) {
+      const float p = expf(al[n] - m);
+      l += p;
+      sp = fmaf(p, gc[n], sp);
+    }
+    l = block_sum(l, scr);
+    sp = block_sum(sp, scr);
+    const float inv_l = 1.0f / l;
+    const float sdot = sp * inv_l;
+    for (int n = tid; n < n_src; n += kBlock) {
+      const float lgn = al[n], r = da[n];
+      const float a = expf(lgn - m) * inv_l;
+      const float dlogit = a * (gc[n] - sdot);
+      al[n] = a;
+      da[n] = dlogit * r;
+      gc[n] = -dlogit * lgn * r * r * inv_d;
+    }
+    __syncthreads();
+    for (int k = tid; k < d; k += kBlock) {
+      const float gk = load_elem(g, tok * d + k, vt);
+      const float wk = load_elem(w, k, wt);
+      float dwk = 0.0f;
+      for (int n = 0; n < n_src; ++n) {
+        const float x = load_elem(v, (int64_t)n * src_stride + tok * d + k, vt);
+        store_elem(dv, (int64_t)n * dv_stride + tok * d + k,
+                   fmaf(gc[n], x, fmaf(da[n], wk, al[n] * gk)), vt);
+        dwk = fmaf(da[n], x, dwk);
+      }
+      prow[k] += dwk;
+    }
+    __syncthreads();
+  }
+}
+
+// dw[c] = sum over rows r of partial[r][c], in a fixed order: wave q of the
+// 1024-thread workgroup sums rows [q*rows/16, (q+1)*rows/16) in sequence, then
+// the 16 wave sums are added in wave order. Same inputs, same bits.
+__global__ void __launch_bounds__(1024)
+k_dw_reduce(const float* __restrict__ partial, int rows, int d, void* __restrict__ dw, int wt) {
+  __shared__ float sh[16][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int col = blockIdx.x * 64 + lane;
+  float s = 0.0f;
+  if (col < d) {
+    const int r0 = (int)((int64_t)wave * rows / 16), r1 = (int)((int64_t)(wave + 1) * rows / 16);
+    for (int r = r0; r < r1; ++r) s += partial[(int64_t)r * d + col];
+  }
+  sh[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0 && col < d) {
+    float t = sh[0][lane];
+#pragma unroll
+    for (int q = 1; q < 16; ++q) t += sh[q][lane];
+    store_elem(dw, col, t, wt);
+  }
+}
+
+// ------------------------------------------------------------------ probes
+
+__global__ void __launch_bounds__(256)
+k_probe_read(const i32x4_t* __restrict__ src, int64_t n16, float* __restrict__ dst) {
+  __shared__ int sh[256];
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  int acc = 0;
+  int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const i32x4_t a = __builtin_nontemporal_load(src + i);
+    const i32x4_t b = __builtin_nontemporal_load(src + i + stride);
+    const i32x4_t c = __builtin_nontemporal_load(src + i + 2 * stride);
+    const i32x4_t e = __builtin_nontemporal_load(src + i + 3 * stride);
+    acc ^= (a.x ^ a.y ^ a.z ^ a.w) ^ (b.x ^ b.y ^ b.z ^ b.w) ^ (c.x ^ c.y ^ c.z ^ c.w) ^
+           (e.x ^ e.y ^ e.z ^ e.w);
+  }
+  for (; i < n16; i += stride) {
+    const i32x4_t a = src[i];
+    acc ^= a.x ^ a.y ^ a.z ^ a.w;
+  }
+  sh[threadIdx.x] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int t = 0;
+    for (int k = 0; k < 256; ++k) t ^= sh[k];
+    dst[blockIdx.x] = (float)t;
+  }
+}
+
+__global__ void __launch_bounds__(256) k_probe_write(i32x4_t* __restrict__ dst, int64_t n16) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  const i32x4_t z = {0x3f800000, 0x3f800000, 0x3f800000, 0x3f800000};
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride)
+    __builtin_nontemporal_store(z, dst + i);
+}
+
+__global__ void __launch_bounds__(256)
+k_probe_copy(const i32x4_t* __restrict__ src, i32x4_t* __restrict__ dst, int64_t n16) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  for (; i + stride < n16; i += 2 * stride) {
+    const i32x4_t a = __builtin_nontemporal_load(src + i);
+    const i32x4_t b = __builtin_nontemporal_load(src + i + stride);
+    __builtin_nontemporal_store(a, dst + i);
+    __builtin_nontemporal_store(b, dst + i + stride);
+  }
+  for (; i < n16; i += stride) dst[i] = src[i];
+}
+
+}  // namespace
+
+hipError_t launch_fwd_generic(const FwdArgs& a, hipStream_t s) {
+  const size_t lds = (size_t)(2 * a.n_src + 257) * sizeof(float);
+  hipLaunchKernelGGL(k_fwd_generic, dim3((unsigned)a.n_tok), dim3(kBlock), lds, s, a.v, a.w, a.out,
+                     a.stats, a.n_src, a.n_tok, a.d, a.src_stride, a.v_dtype, a.w_dtype, a.eps,
+                     1.0f / (float)a.d);
+  return hipGetLastError();
+}
+
+hipError_t launch_sol_generic(const FwdArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(k_sol_generic, dim3((unsigned)a.n_tok), dim3(kBlock), 0, s, a.v, a.out,
+                     a.n_src, a.n_tok, a.d, a.src_stride, a.v_dtype);
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd_generic(const BwdArgs& a, int grid, hipStream_t s) {
+  const size_t lds = (size_t)(3 * a.n_src + 257) * sizeof(float);
+  hipLaunchKernelGGL(k_bwd_generic, dim3(grid), dim3(kBlock), lds, s, a.v, a.w, a.g, a.dv,
+                     a.partial, a.n_src, a.n_tok, a.d, a.src_stride, a.v_dtype, a.w_dtype, a.eps,
+                     1.0f / (float)a.d);
+  return hipGetLastError();
+}
+
+hipError_t launch_dw_reduce(const float* partial, int rows, int d, void* dw, int w_dtype,
+                            hipStream_t s) {
+  hipLaunchKernelGGL(k_dw_reduce, dim3((unsigned)((d + 63) / 64)), dim3(1024), 0, s, partial, rows,
+                     d, dw, w_dtype);
+  return hipGetLastError();
+}
+
+hipError_t launch_probe(int kind, const void* src, void* dst, int64_t bytes, int grid,
+                        hipStream_t s) {
+  const int64_t n16 = bytes / 16;
+  if (kind == 0) {
+    hipLaunchKernelGGL(k_probe_read, dim3(grid), dim3(256), 0, s, (const i32x4_t*)src, n16,
+                       (float*)dst);
+  } else if (kind == 1) {
+    hipLaunchKernelGGL(k_probe_write, dim3(grid), dim3(256), 0, s, (i32x4_t*)dst, n16);
+  } else {
+    hipLaunchKernelGGL(k_probe_copy, dim3(grid), dim3(256), 0, s, (const i32x4_t*)src,
+                       (i32x4_t*)dst, n16);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace sy

@@ -1,0 +1,552 @@
+// Register-tiled Block AttnRes kernels for gfx950.
+//
+// Geometry. A token's [N, D] tile is spread over W wavefronts: lane l of wave
+// `seg` owns the 16-byte chunks c = (seg*64 + l) + j*64*W, j < VPL, of every
+// source row, so each buffer_load_dwordx4 of a wave reads 1 KiB of contiguous
+// row memory. Rows past N are never loaded; chunks past the row end read as 0
+// through the buffer descriptor's range check and are never stored.
+//
+// Per token the kernels need only 2-3 wave-uniform scalars per source row
+// (sum of squares, query dot, grad dot). They are summed with DPP inside each
+// wave; when W > 1 the W partial sums meet in LDS and are added in segment
+// order, so every wave of the token computes bit-identical softmax weights.
+//
+// Reference: src/switchyard/triton_op.py:50-78 (_fwd_resident),
+// :81-117 (_fwd_tiled), :153-191 (_speed_of_light), :194-264 (_bwd_resident),
+// :378-414 (_fwd_batched_resident). The tiling, the online merge across row
+// chunks and the deterministic dw reduction are this build's own design.
+#pragma once
+
+#include "sy_device.hpp"
+
+namespace sy {
+
+// Forward-shaped kernels: 256-thread workgroups (or one token per workgroup
+// when a token needs more than four waves).
+template <int W>
+struct FwdGeom {
+  static constexpr int kBlock = (64 * W > 256) ? 64 * W : 256;
+  static constexpr int kTpb = kBlock / (64 * W);
+};
+
+// Backward: persistent 512-thread workgroups (two waves per SIMD at most
+// 256 VGPRs each); kTpb token slots run side by side.
+template <int W>
+struct BwdGeom {
+  static constexpr int kBlock = 512;
+  static constexpr int kTpb = 512 / (64 * W);
+};
+
+// Sum wave-uniform per-row values across the W waves of each token slot.
+// vals is G groups of NR rows (vals[grp*NR + n]); entries with grp < groups and
+// n < rows take part. Lane 0 of every wave publishes; after one barrier each
+// wave adds the W contributions in segment order. `buf` must not be rewritten
+// until every wave has passed the next barrier, which callers ensure by
+// alternating two buffers. All register indices are compile-time constants.
+template <int W, int G, int NR, int TPB>
+__device__ __forceinline__ void cross_wave_sum(float (&vals)[G * NR], int groups, int rows,
+                                               float (&buf)[TPB][W][G * NR], int slot, int seg,
+                                               int lane) {
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < G * NR; ++i)
+      if (i / NR < groups && i % NR < rows) buf[slot][seg][i] = vals[i];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < G * NR; ++i) {
+    if (i / NR < groups && i % NR < rows) {
+      float s = buf[slot][0][i];
+#pragma unroll
+      for (int k = 1; k < W; ++k) s += buf[slot][k][i];
+      vals[i] = s;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ forward
+//
+// One token per W waves. Rows are processed in chunks of NR; when N <= NR
+// there is one chunk and v is read exactly once with no rescaling. Larger N
+// merges chunks with the online-softmax update (running max m, running sum l,
+// accumulator rescaled by exp(m_old - m_new)), which still reads v once.
+//
+// Optional stats: stats[n*n_tok + t] = logit, stats[(N+n)*n_tok + t] = r_n.
+template <class T, int W, int VPL, int NR>
+__global__ void __launch_bounds__(FwdGeom<W>::kBlock)
+k_fwd(const typename T::storage* __restrict__ v, const typename T::storage* __restrict__ w,
+      typename T::storage* __restrict__ out, float* __restrict__ stats, int n_src,
+      int64_t n_tok, int d, int64_t src_stride, float eps, float inv_d) {
+  using S = typename T::storage;
+  constexpr int CE = T::ce;
+  constexpr int TPB = FwdGeom<W>::kTpb;
+  constexpr uint32_t kStep = 64u * W * 16u;
+  __shared__ float red[2][TPB][W][2 * NR];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int slot = wave / W;
+  const int seg = wave % W;
+  int64_t tok = (int64_t)blockIdx.x * TPB + slot;
+  const bool live = tok < n_tok;
+  if constexpr (W == 1 || TPB == 1) {
+    if (!live) return;  // no barrier is shared with another token slot
+  }
+  if (!live) tok = n_tok - 1;  // keep the slot's waves in step for the barriers
+
+  const uint32_t row_bytes = (uint32_t)d * sizeof(S);
+  const uint32_t lane_off = (uint32_t)(seg * 64 + lane) * 16u;
+
+  i32x4_t wq[VPL];
+  {
+    const auto wr = make_rsrc(w, row_bytes);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) wq[j] = ld16(wr, lane_off + j * kStep);
+  }
+
+  float m_run = -INFINITY, l_run = 0.0f;
+  float acc[VPL][CE];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j)
+#pragma unroll
+    for (int e = 0; e < CE; ++e) acc[j][e] = 0.0f;
+
+  int it = 0;
+  for (int c0 = 0; c0 < n_src; c0 += NR, ++it) {
+    const int rows = min(NR, n_src - c0);
+    i32x4_t x[NR][VPL];
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      if (n < rows) {
+        const auto r = make_rsrc(v + (int64_t)(c0 + n) * src_stride + tok * d, row_bytes);
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) x[n][j] = ld16(r, lane_off + j * kStep);
+      }
+    }
+
+    // part[n] = sum of squares, part[NR + n] = query dot of row c0 + n.
+    float part[2 * NR];
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      if (n < rows) {
+        float ss = 0.0f, dt = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+          ss = dot<T>(x[n][j], x[n][j], ss);
+          dt = dot<T>(x[n][j], wq[j], dt);
+        }
+        part[n] = wave_sum(ss);
+        part[NR + n] = wave_sum(dt);
+      }
+    }
+    if constexpr (W > 1) cross_wave_sum<W, 2, NR, TPB>(part, 2, rows, red[it & 1], slot, seg, lane);
+
+    float lg[NR];
+    float cm = m_run;
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      if (n < rows) {
+        const float r = rsqrtf(fmaf(part[n], inv_d, eps));
+        lg[n] = part[NR + n] * r;
+        cm = fmaxf(cm, lg[n]);
+        if (stats != nullptr && seg == 0 && lane == 0 && live) {
+          stats[(int64_t)(c0 + n) * n_tok + tok] = lg[n];
+          stats[(int64_t)(n_src + c0 + n) * n_tok + tok] = r;
+        }
+      }
+    }
+    if (it > 0) {
+      const float sc = expf(m_run - cm);
+      l_run *= sc;
+#pragma unroll
+      for (int j = 0; j < VPL; ++j)
+#pragma unroll
+        for (int e = 0; e < CE; ++e) acc[j][e] *= sc;
+    }
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      if (n < rows) {
+        const float p = expf(lg[n] - cm);
+        l_run += p;
+#pragma unroll
+        for (int j = 0; j < VPL; ++j)
+#pragma unroll
+          for (int e = 0; e < CE; ++e) acc[j][e] = fmaf(p, elem<T>(x[n][j], e), acc[j][e]);
+      }
+    }
+    m_run = cm;
+  }
+
+  if (!live) return;
+  const float inv_l = 1.0f / l_run;
+  const auto orr = make_rsrc(out + tok * d, row_bytes);
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    float f[CE];
+#pragma unroll
+    for (int e = 0; e < CE; ++e) f[e] = acc[j][e] * inv_l;
+    st16(orr, lane_off + j * kStep, pack<T>(f));
+  }
+}
+
+// ------------------------------------------------------------ speed of light
+//
+// Same bytes, geometry and launch shape as k_fwd, no softmax: out = sum_n v_n.
+template <class T, int W, int VPL, int NR>
+__global__ void __launch_bounds__(FwdGeom<W>::kBlock)
+k_sol(const typename T::storage* __restrict__ v, typename T::storage* __restrict__ out, int n_src,
+      int64_t n_tok, int d, int64_t src_stride) {
+  using S = typename T::storage;
+  constexpr int CE = T::ce;
+  constexpr int TPB = FwdGeom<W>::kTpb;
+  constexpr uint32_t kStep = 64u * W * 16u;
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int64_t tok = (int64_t)blockIdx.x * TPB + wave / W;
+  if (tok >= n_tok) return;
+  const uint32_t row_bytes = (uint32_t)d * sizeof(S);
+  const uint32_t lane_off = (uint32_t)((wave % W) * 64 + lane) * 16u;
+
+  float acc[VPL][CE];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j)
+#pragma unroll
+    for (int e = 0; e < CE; ++e) acc[j][e] = 0.0f;
+  for (int c0 = 0; c0 < n_src; c0 += NR) {
+    const int rows = min(NR, n_src - c0);
+    i32x4_t x[NR][VPL];
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      if (n < rows) {
+        const auto r = make_rsrc(v + (int64_t)(c0 + n) * src_stride + tok * d, row_bytes);
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) x[n][j] = ld16(r, lane_off + j * kStep);
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < NR; ++n)
+      if (n < rows)
+#pragma unroll
+        for (int j = 0; j < VPL; ++j)
+#pragma unroll
+          for (int e = 0; e < CE; ++e) acc[j][e] += elem<T>(x[n][j], e);
+  }
+  const auto orr = make_rsrc(out + tok * d, row_bytes);
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) st16(orr, lane_off + j * kStep, pack<T>(acc[j]));
+}
+
+// ----------------------------------------------------------------- batched
+//
+// S queries against one register-resident tile (N <= NR): the inverse RMS of
+// each row is computed once, then each query costs one dot reduction per row,
+// a softmax and a weighted sum. v is read once for all S outputs.
+template <class T, int W, int VPL, int NR>
+__global__ void __launch_bounds__(FwdGeom<W>::kBlock)
+k_batched(const typename T::storage* __restrict__ v, const typename T::storage* __restrict__ q,
+          typename T::storage* __restrict__ out, int n_src, int n_q, int64_t n_tok, int d,
+          int64_t src_stride, float eps, float inv_d) {
+  using S = typename T::storage;
+  constexpr int CE = T::ce;
+  constexpr int TPB = FwdGeom<W>::kTpb;
+  constexpr uint32_t kStep = 64u * W * 16u;
+  __shared__ float red[2][TPB][W][NR];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int slot = wave / W;
+  const int seg = wave % W;
+  int64_t tok = (int64_t)blockIdx.x * TPB + slot;
+  const bool live = tok < n_tok;
+  if constexpr (W == 1 || TPB == 1) {
+    if (!live) return;
+  }
+  if (!live) tok = n_tok - 1;
+  const uint32_t row_bytes = (uint32_t)d * sizeof(S);
+  const uint32_t lane_off = (uint32_t)(seg * 64 + lane) * 16u;
+  const int rows = n_src;  // host guarantees n_src <= NR
+
+  i32x4_t x[NR][VPL];
+#pragma unroll
+  for (int n = 0; n < NR; ++n) {
+    if (n < rows) {
+      const auto r = make_rsrc(v + (int64_t)n * src_stride + tok * d, row_bytes);
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) x[n][j] = ld16(r, lane_off + j * kStep);
+    }
+  }
+  float rinv[NR];
+#pragma unroll
+  for (int n = 0; n < NR; ++n) {
+    if (n < rows) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) ss = dot<T>(x[n][j], x[n][j], ss);
+      rinv[n] = wave_sum(ss);
+    }
+  }
+  int it = 0;
+  if constexpr (W > 1) cross_wave_sum<W, 1, NR, TPB>(rinv, 1, rows, red[it++ & 1], slot, seg, lane);
+#pragma unroll
+  for (int n = 0; n < NR; ++n)
+    if (n < rows) rinv[n] = rsqrtf(fmaf(rinv[n], inv_d, eps));
+
+  for (int s = 0; s < n_q; ++s) {
+    i32x4_t qq[VPL];
+    const auto qr = make_rsrc(q + (int64_t)s * d, row_bytes);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) qq[j] = ld16(qr, lane_off + j * kStep);
+    float lg[NR];
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      if (n < rows) {
+        float dt = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) dt = dot<T>(x[n][j], qq[j], dt);
+        lg[n] = wave_sum(dt);
+      }
+    }
+    if constexpr (W > 1) cross_wave_sum<W, 1, NR, TPB>(lg, 1, rows, red[it++ & 1], slot, seg, lane);
+    float m = -INFINITY;
+#pragma unroll
+    for (int n = 0; n < NR; ++n)
+      if (n < rows) {
+        lg[n] *= rinv[n];
+        m = fmaxf(m, lg[n]);
+      }
+    float l = 0.0f;
+    float acc[VPL][CE];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+#pragma unroll
+      for (int e = 0; e < CE; ++e) acc[j][e] = 0.0f;
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      if (n < rows) {
+        const float p = expf(lg[n] - m);
+        l += p;
+#pragma unroll
+        for (int j = 0; j < VPL; ++j)
+#pragma unroll
+          for (int e = 0; e < CE; ++e) acc[j][e] = fmaf(p, elem<T>(x[n][j], e), acc[j][e]);
+      }
+    }
+    if (live) {
+      const float inv_l = 1.0f / l;
+      const auto orr = make_rsrc(out + ((int64_t)s * n_tok + tok) * d, row_bytes);
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) {
+        float f[CE];
+#pragma unroll
+        for (int e = 0; e < CE; ++e) f[e] = acc[j][e] * inv_l;
+        st16(orr, lane_off + j * kStep, pack<T>(f));
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------------- backward
+//
+// Persistent: workgroup b owns token slots b*TPB + slot + k*gridDim.x*TPB for
+// k < n_iter (the same trip count for every slot, so barriers line up; slots
+// past the end re-read the last token and store nothing). Per token, with
+// r_n = rsqrt(ssq_n/D + eps), logit_n = a_n r_n, alpha = softmax(logit),
+// G_n = <g, v_n> (derivation of triton_op.py:205-214):
+//     S        = sum_n alpha_n G_n
+//     dlogit_n = alpha_n (G_n - S)
+//     da_n     = dlogit_n r_n
+//     c_n      = 2 dssq_n = -dlogit_n a_n r_n^3 / D = -dlogit_n logit_n r_n^2 / D
+//     dv_n     = alpha_n g + da_n w + c_n v_n
+//     dw      += sum_n da_n v_n
+// With stats (logit_n, r_n from the forward) only G_n is reduced over D.
+// dw: each slot accumulates in registers; at the end the slots are folded in
+// a fixed tree through LDS and the workgroup writes one fp32 row of `partial`.
+// No float atomics anywhere, so dw is bit-reproducible for a given grid.
+template <class T, int W, int VPL, int NR>
+__global__ void __launch_bounds__(BwdGeom<W>::kBlock)
+k_bwd(const typename T::storage* __restrict__ v, const typename T::storage* __restrict__ w,
+      const typename T::storage* __restrict__ g, const float* __restrict__ stats,
+      typename T::storage* __restrict__ dv, float* __restrict__ partial, int n_src, int64_t n_tok,
+      int d, int64_t src_stride, float eps, float inv_d, int n_iter) {
+  using S = typename T::storage;
+  constexpr int CE = T::ce;
+  constexpr int TPB = BwdGeom<W>::kTpb;
+  constexpr uint32_t kStep = 64u * W * 16u;
+  constexpr int kLaneFloats = VPL * CE;  // dw values a lane accumulates
+  // Slot fold buffer: the upper half of the live slots parks its dw here. The
+  // +1 pad keeps the lane-strided writes free of bank conflicts.
+  constexpr int kFH = TPB > 1 ? TPB / 2 : 1;
+  constexpr int kFW = TPB > 1 ? W : 1;
+  constexpr int kFL = TPB > 1 ? 64 : 1;
+  __shared__ float red[2][TPB][W][3 * NR];
+  __shared__ float fold[kFH][kFW][kFL][kLaneFloats + 1];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int slot = wave / W;
+  const int seg = wave % W;
+  const uint32_t row_bytes = (uint32_t)d * sizeof(S);
+  const uint32_t lane_off = (uint32_t)(seg * 64 + lane) * 16u;
+  const int64_t slots = (int64_t)gridDim.x * TPB;
+  const int64_t dv_stride = n_tok * d;
+  const int rows = n_src;  // host guarantees n_src <= NR
+
+  i32x4_t wq[VPL];
+  {
+    const auto wr = make_rsrc(w, row_bytes);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) wq[j] = ld16(wr, lane_off + j * kStep);
+  }
+  float dwa[VPL][CE];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j)
+#pragma unroll
+    for (int e = 0; e < CE; ++e) dwa[j][e] = 0.0f;
+
+  for (int k = 0; k < n_iter; ++k) {
+    int64_t tok = (int64_t)blockIdx.x * TPB + slot + k * slots;
+    const bool live = tok < n_tok;
+    if (!live) tok = n_tok - 1;
+
+    i32x4_t x[NR][VPL];
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      if (n < rows) {
+        const auto r = make_rsrc(v + (int64_t)n * src_stride + tok * d, row_bytes);
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) x[n][j] = ld16(r, lane_off + j * kStep);
+      }
+    }
+    i32x4_t gq[VPL];
+    {
+      const auto gr = make_rsrc(g + tok * d, row_bytes);
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) gq[j] = ld16(gr, lane_off + j * kStep);
+    }
+
+    // Per-row scalars: part[n] grad dot, then (without stats) part[NR + n]
+    // query dot and part[2*NR + n] sum of squares.
+    const bool have_stats = stats != nullptr;
+    float part[3 * NR];
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      if (n < rows) {
+        float gg = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) gg = dot<T>(x[n][j], gq[j], gg);
+        part[n] = wave_sum(gg);
+        if (!have_stats) {
+          float dt = 0.0f, ss = 0.0f;
+#pragma unroll
+          for (int j = 0; j < VPL; ++j) {
+            dt = dot<T>(x[n][j], wq[j], dt);
+            ss = dot<T>(x[n][j], x[n][j], ss);
+          }
+          part[NR + n] = wave_sum(dt);
+          part[2 * NR + n] = wave_sum(ss);
+        }
+      }
+    }
+    if constexpr (W > 1)
+      cross_wave_sum<W, 3, NR, TPB>(part, have_stats ? 1 : 3, rows, red[k & 1], slot, seg, lane);
+
+    float lg[NR], rr[NR];
+    float m = -INFINITY;
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      if (n < rows) {
+        if (have_stats) {
+          lg[n] = stats[(int64_t)n * n_tok + tok];
+          rr[n] = stats[(int64_t)(n_src + n) * n_tok + tok];
+        } else {
+          rr[n] = rsqrtf(fmaf(part[2 * NR + n], inv_d, eps));
+          lg[n] = part[NR + n] * rr[n];
+        }
+        m = fmaxf(m, lg[n]);
+      }
+    }
+    float al[NR];
+    float l = 0.0f;
+#pragma unroll
+    for (int n = 0; n < NR; ++n)
+      if (n < rows) {
+        al[n] = expf(lg[n] - m);
+        l += al[n];
+      }
+    const float inv_l = 1.0f / l;
+    float sdot = 0.0f;
+#pragma unroll
+    for (int n = 0; n < NR; ++n)
+      if (n < rows) {
+        al[n] *= inv_l;
+        sdot = fmaf(al[n], part[n], sdot);
+      }
+
+    float gf[VPL][CE], wf[VPL][CE];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+#pragma unroll
+      for (int e = 0; e < CE; ++e) {
+        gf[j][e] = elem<T>(gq[j], e);
+        wf[j][e] = elem<T>(wq[j], e);
+      }
+    const float dw_on = live ? 1.0f : 0.0f;
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      if (n < rows) {
+        const float dlogit = al[n] * (part[n] - sdot);
+        const float da = dlogit * rr[n];
+        const float c = -dlogit * lg[n] * rr[n] * rr[n] * inv_d;
+        const float da_w = da * dw_on;
+        const auto dr = make_rsrc(dv + (int64_t)n * dv_stride + tok * d, live ? row_bytes : 0u);
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+          float f[CE];
+#pragma unroll
+          for (int e = 0; e < CE; ++e) {
+            const float xv = elem<T>(x[n][j], e);
+            f[e] = fmaf(c, xv, fmaf(da, wf[j][e], al[n] * gf[j][e]));
+            dwa[j][e] = fmaf(da_w, xv, dwa[j][e]);
+          }
+          st16(dr, lane_off + j * kStep, pack<T>(f));
+        }
+      }
+    }
+  }
+
+  // Fold the TPB slot accumulators: slots [h, 2h) add into [0, h), h halving.
+#pragma unroll
+  for (int h = TPB / 2; h >= 1; h /= 2) {
+    __syncthreads();
+    if (slot >= h && slot < 2 * h) {
+#pragma unroll
+      for (int j = 0; j < VPL; ++j)
+#pragma unroll
+        for (int e = 0; e < CE; ++e) fold[slot - h][seg][lane][j * CE + e] = dwa[j][e];
+    }
+    __syncthreads();
+    if (slot < h) {
+#pragma unroll
+      for (int j = 0; j < VPL; ++j)
+#pragma unroll
+        for (int e = 0; e < CE; ++e) dwa[j][e] += fold[slot][seg][lane][j * CE + e];
+    }
+  }
+  if (slot == 0) {
+    const auto pr = make_rsrc(partial + (int64_t)blockIdx.x * d, (uint32_t)d * 4u);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      // chunk c covers elements [c*CE, c*CE + CE): CE/4 float4 stores
+      const uint32_t base = (lane_off / 16u + j * 64u * W) * CE * 4u;
+#pragma unroll
+      for (int q4 = 0; q4 < CE / 4; ++q4) {
+        i32x4_t t;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[e] = __float_as_int(dwa[j][q4 * 4 + e]);
+        st16(pr, base + q4 * 16u, t);
+      }
+    }
+  }
+}
+
+}  // namespace sy

@@ -1,0 +1,153 @@
+// Shape -> kernel plan. Pure arithmetic, no device access, so the CPU test
+// suite can pin the dispatch rules (the reference pins its own in
+// tests/test_triton_op.py:145-148 and :271-288).
+//
+// Rules, in order:
+//  1. Vector kernels need every row start 16-byte aligned, D a multiple of the
+//     chunk width, and (forward/backward) w in v's dtype. Otherwise: generic.
+//  2. Prefer the fewest waves per token whose chunks-per-lane is 1, 2 or 4 and
+//     whose resident tile (rows_per_tile x chunks_per_lane 16-byte chunks,
+//     four VGPRs each) fits the op's budget with rows_per_tile >= N.
+//  3. Forward / speed-of-light with no resident fit: online-softmax chunks of
+//     the largest tile that fits.
+//  4. Backward with no resident fit under its budget: generic (a fatter tile
+//     would spill: the backward runs two waves per SIMD at most 256 VGPRs).
+//  5. Batched: resident with S <= 16, else one forward launch per query.
+#include <cstdio>
+#include <cstdlib>
+
+#include "../../include/switchyard.h"
+#include "sy_launch.hpp"
+
+namespace sy {
+
+namespace {
+
+// Resident tile budget in 16-byte chunks per lane (4 VGPRs each). The
+// backward also keeps grad_out, w, their fp32 copies and dw accumulators live,
+// and the batched kernel a query and an accumulator, so both take a thinner
+// tile (more waves per token) than the forward.
+constexpr int kFwdBudget = 36;
+constexpr int kBwdBudget = 18;
+constexpr int kBatchedBudget = 18;
+constexpr int kWaves[] = {1, 2, 4, 8};
+constexpr int kRows[] = {4, 9, 16};
+
+bool valid_dtype(int t) { return t == SY_F32 || t == SY_F16 || t == SY_BF16; }
+
+int round_vpl(int64_t v) { return v <= 1 ? 1 : (v <= 2 ? 2 : (v <= 4 ? 4 : 0)); }
+
+bool tile_exists(int vpl, int nr) { return !(vpl == 4 && nr == 16); }
+
+void set(sy_plan* p, int family, int w, int vpl, int nr, int ce, int op, int64_t n_src) {
+  p->family = family;
+  p->waves_per_token = w;
+  p->chunks_per_lane = vpl;
+  p->rows_per_tile = nr;
+  p->elems_per_chunk = ce;
+  if (family == SY_FAMILY_GENERIC) {
+    p->block_threads = 256;
+    p->tokens_per_block = 1;
+    p->n_chunks = 1;
+    return;
+  }
+  if (op == SY_OP_BWD) {
+    p->block_threads = 512;
+    p->tokens_per_block = 512 / (64 * w);
+  } else {
+    p->block_threads = 64 * w > 256 ? 64 * w : 256;
+    p->tokens_per_block = p->block_threads / (64 * w);
+  }
+  p->n_chunks = (int)((n_src + nr - 1) / nr);
+}
+
+// Resident plan with rows_per_tile >= n_src under `budget`; false if none.
+bool resident(int64_t n_src, int64_t e, int budget, int* w_out, int* vpl_out, int* nr_out) {
+  for (int w : kWaves) {
+    const int vpl = round_vpl((e + 64 * w - 1) / (64 * w));
+    if (vpl == 0) continue;
+    for (int nr : kRows) {
+      if (!tile_exists(vpl, nr) || nr < n_src || nr * vpl > budget) continue;
+      *w_out = w;
+      *vpl_out = vpl;
+      *nr_out = nr;
+      return true;
+    }
+  }
+  return false;
+}
+
+}  // namespace
+
+int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_dtype,
+              int aligned, sy_plan* out) {
+  if (out == nullptr) return SY_ERR_NULL;
+  if (op < SY_OP_FWD || op > SY_OP_SOL) return SY_ERR_OP;
+  if (!valid_dtype(v_dtype) || !valid_dtype(w_dtype)) return SY_ERR_DTYPE;
+  if (n_src < 1 || d < 1 || (op == SY_OP_BATCHED && n_q < 1)) return SY_ERR_SHAPE;
+  if (n_src > 0x7fffffff || d > 0x7fffffff / 16) return SY_ERR_SHAPE;
+
+  const int ce = v_dtype == SY_F32 ? 4 : 8;
+  const bool same_w = op == SY_OP_SOL || op == SY_OP_BATCHED || v_dtype == w_dtype;
+  const bool vec = aligned && (d % ce == 0) && same_w;
+  const int64_t e = d / ce;
+  int w = 0, vpl = 0, nr = 0;
+
+  if (vec && !(op == SY_OP_BATCHED && n_q > kBatchedMaxQ)) {
+    const int budget =
+        op == SY_OP_BWD ? kBwdBudget : (op == SY_OP_BATCHED ? kBatchedBudget : kFwdBudget);
+    if (resident(n_src, e, budget, &w, &vpl, &nr)) {
+      set(out, SY_FAMILY_RESIDENT, w, vpl, nr, ce, op, n_src);
+      return SY_OK;
+    }
+    if (op == SY_OP_FWD || op == SY_OP_SOL) {
+      for (int ww : kWaves) {
+        const int v2 = round_vpl((e + 64 * ww - 1) / (64 * ww));
+        if (v2 == 0) continue;
+        set(out, SY_FAMILY_CHUNKED, ww, v2, v2 == 4 ? 9 : 16, ce, op, n_src);
+        return SY_OK;
+      }
+    }
+  }
+  if (op == SY_OP_BATCHED) {
+    // Per-query forward launches; report the plan each of them uses.
+    const int rc = make_plan(SY_OP_FWD, n_src, 0, d, v_dtype, v_dtype, aligned, out);
+    if (rc != SY_OK) return rc;
+    out->family = SY_FAMILY_PER_QUERY;
+    return SY_OK;
+  }
+  if ((op == SY_OP_FWD || op == SY_OP_BWD) && n_src > kGenericMaxN) return SY_ERR_SHAPE;
+  set(out, SY_FAMILY_GENERIC, 4, 0, 0, 1, op, n_src);
+  return SY_OK;
+}
+
+bool tile_listed(int w, int vpl, int nr) {
+#define X(W_, V_, N_) \
+  if (w == W_ && vpl == V_ && nr == N_) return true;
+  SY_TILES(X)
+#undef X
+  return false;
+}
+
+// Tuning knob for measurement sweeps: SY_TILE_FWD / SY_TILE_BWD /
+// SY_TILE_BATCHED / SY_TILE_SOL = "W,VPL,NR" replaces the tile of a vector
+// plan when that tile is built, covers the row, and (backward, batched) holds
+// every row. Anything else leaves the plan untouched.
+void apply_tile_override(int op, int64_t n_src, int64_t d, sy_plan* p) {
+  if (p->family != SY_FAMILY_RESIDENT && p->family != SY_FAMILY_CHUNKED) return;
+  const char* name = op == SY_OP_FWD ? "SY_TILE_FWD"
+                     : op == SY_OP_BWD ? "SY_TILE_BWD"
+                     : op == SY_OP_BATCHED ? "SY_TILE_BATCHED"
+                                           : "SY_TILE_SOL";
+  const char* s = std::getenv(name);
+  int w = 0, vpl = 0, nr = 0;
+  if (s == nullptr || std::sscanf(s, "%d,%d,%d", &w, &vpl, &nr) != 3) return;
+  if (!tile_listed(w, vpl, nr)) return;
+  if ((int64_t)64 * w * vpl < d / p->elems_per_chunk) return;
+  const bool can_chunk = op == SY_OP_FWD || op == SY_OP_SOL;
+  if (nr < n_src && !can_chunk) return;
+  set(p, nr >= n_src ? SY_FAMILY_RESIDENT : SY_FAMILY_CHUNKED, w, vpl, nr, p->elems_per_chunk, op,
+      n_src);
+}
+
+}  // namespace sy

@@ -1,0 +1,120 @@
+"""ctypes binding of ``libswitchyard_hip.so`` (the C ABI in include/switchyard.h).
+
+The library is loaded after ``import torch`` so that it binds to the HIP
+runtime torch already loaded (same ``libamdhip64.so.7`` soname): one runtime
+per process. It is built in-tree by ``make -C blackwell-switchyard_amd/csrc``
+(or ``__graft_entry__.build()``). There is no fallback: if the library is
+missing every operator raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import threading
+
+import torch  # noqa: F401  -- must precede the load: provides the HIP runtime
+
+LIB_PATH = pathlib.Path(__file__).resolve().parent / "libswitchyard_hip.so"
+
+SY_F32, SY_F16, SY_BF16 = 0, 1, 2
+OP_FWD, OP_BWD, OP_BATCHED, OP_SOL = 0, 1, 2, 3
+FAMILY_NAMES = {0: "resident", 1: "chunked", 2: "generic", 3: "per_query"}
+
+_DTYPE_CODES = {torch.float32: SY_F32, torch.float16: SY_F16, torch.bfloat16: SY_BF16}
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+
+
+class Plan(ctypes.Structure):
+    """Mirror of ``sy_plan``."""
+
+    _fields_ = [
+        ("family", ctypes.c_int32),
+        ("waves_per_token", ctypes.c_int32),
+        ("chunks_per_lane", ctypes.c_int32),
+        ("rows_per_tile", ctypes.c_int32),
+        ("elems_per_chunk", ctypes.c_int32),
+        ("block_threads", ctypes.c_int32),
+        ("tokens_per_block", ctypes.c_int32),
+        ("n_chunks", ctypes.c_int32),
+    ]
+
+    def as_dict(self) -> dict:
+        d = {name: int(getattr(self, name)) for name, _ in self._fields_}
+        d["family_name"] = FAMILY_NAMES.get(d["family"], "?")
+        return d
+
+
+#: Every symbol include/switchyard.h declares, with (restype, argtypes).
+SIGNATURES = {
+    "sy_abi_version": (_i32, []),
+    "sy_plan_for": (_i32, [_i32, _i64, _i64, _i64, _i32, _i32, _i32, ctypes.POINTER(Plan)]),
+    "sy_fwd": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32, ctypes.c_float, _vp]),
+    "sy_bwd_workspace_bytes": (_i64, [_i64, _i64, _i64, _i32, _i32]),
+    "sy_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32, _i32,
+                      ctypes.c_float, _vp]),
+    "sy_fwd_batched": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32, ctypes.c_float, _vp]),
+    "sy_sol": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp]),
+    "sy_bw_probe": (_i32, [_i32, _vp, _vp, _i64, _vp]),
+    "sy_probe_grid": (_i64, [_i64]),
+    "sy_strerror": (ctypes.c_char_p, [_i32]),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library with typed entry points. Raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"switchyard HIP library not found at {LIB_PATH}; build it with "
+                    "`make -C blackwell-switchyard_amd/csrc` (there is no fallback path)"
+                )
+            so = ctypes.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(so, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = so
+    return _lib
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODES[dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {dtype}; expected bfloat16, float16 or float32") from None
+
+
+def strerror(rc: int) -> str:
+    return lib().sy_strerror(rc).decode()
+
+
+def check(rc: int, what: str) -> None:
+    """Raise RuntimeError for a nonzero C-ABI status."""
+    if rc != 0:
+        raise RuntimeError(f"{what} failed ({rc}): {strerror(rc)}")
+
+
+def plan(op: int, n_src: int, d: int, dtype: torch.dtype, *, n_q: int = 0,
+         w_dtype: torch.dtype | None = None, aligned: bool = True) -> dict:
+    """The execution plan the library picks for a shape (pure host arithmetic)."""
+    p = Plan()
+    rc = lib().sy_plan_for(op, n_src, n_q, d, dtype_code(dtype), dtype_code(w_dtype or dtype),
+                           int(aligned), ctypes.byref(p))
+    check(rc, "sy_plan_for")
+    return p.as_dict()
+
+
+def stream_ptr(device: torch.device) -> ctypes.c_void_p:
+    """The HIP stream torch is currently issuing work on for ``device``."""
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)

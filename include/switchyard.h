@@ -1,0 +1,143 @@
+/*
+ * switchyard for MI355X -- C ABI of the Block AttnRes operator.
+ *
+ * One token (b, t) of the operator, with N sources v_0..v_{N-1} of width D and
+ * a pseudo-query w:
+ *
+ *     r_n     = 1 / sqrt(mean_d(v_n[d]^2) + eps)
+ *     logit_n = r_n * sum_d w[d] * v_n[d]          (no 1/sqrt(D) factor)
+ *     alpha   = softmax_n(logit)                   (over the source axis)
+ *     out[d]  = sum_n alpha_n * v_n[d]              (weighted sum of RAW sources)
+ *
+ * Layout (all element counts, not bytes):
+ *   v        [N][n_tok][D]  row n of token t at v + n*src_stride + t*D
+ *   out      [n_tok][D]     contiguous
+ *   grad_out [n_tok][D]     contiguous, same dtype as v
+ *   dv       [N][n_tok][D]  contiguous (source stride n_tok*D)
+ *   w, dw    [D]
+ *   queries  [S][D], batched out [S][n_tok][D]
+ * n_tok is B*T: the batch and sequence axes are flattened because tokens are
+ * independent.
+ *
+ * Conventions shared by every entry point:
+ *   - Launches are asynchronous on `stream` (a hipStream_t; NULL = the null
+ *     stream). Nothing synchronises the host.
+ *   - The library never allocates device memory: the caller owns every buffer,
+ *     including the backward workspace sized by sy_bwd_workspace_bytes().
+ *   - Return value 0 = success; < 0 = an sy_status argument error detected
+ *     before any device work; > 0 = the hipError_t the HIP runtime returned.
+ *   - Entry points are reentrant; concurrent calls on different streams are
+ *     safe as long as they do not share output or workspace buffers.
+ */
+#ifndef SWITCHYARD_H
+#define SWITCHYARD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SY_ABI_VERSION 1
+
+/* Element types. Reference: tensors may be bf16/fp16/fp32 and all arithmetic is
+ * fp32 (src/switchyard/triton_op.py:36, :66-67). */
+typedef enum sy_dtype { SY_F32 = 0, SY_F16 = 1, SY_BF16 = 2 } sy_dtype;
+
+typedef enum sy_status {
+  SY_OK = 0,
+  SY_ERR_NULL = -1,        /* a required pointer is NULL                       */
+  SY_ERR_SHAPE = -2,       /* a size is out of range (N < 1, D < 1, ...)       */
+  SY_ERR_DTYPE = -3,       /* unknown dtype code or unsupported combination    */
+  SY_ERR_WORKSPACE = -4,   /* workspace NULL or smaller than required          */
+  SY_ERR_STRIDE = -5,      /* src_stride < n_tok * D                           */
+  SY_ERR_DEVICE = -6,      /* no usable HIP device                             */
+  SY_ERR_OP = -7           /* unknown operation or probe kind                  */
+} sy_status;
+
+/* Operations known to sy_plan(). */
+typedef enum sy_op { SY_OP_FWD = 0, SY_OP_BWD = 1, SY_OP_BATCHED = 2, SY_OP_SOL = 3 } sy_op;
+
+/* Kernel families a plan can select. */
+typedef enum sy_family {
+  SY_FAMILY_RESIDENT = 0,  /* the whole [N, D] token tile lives in registers       */
+  SY_FAMILY_CHUNKED = 1,   /* register tile of NR rows, online softmax over chunks */
+  SY_FAMILY_GENERIC = 2,   /* element-wise loads, two passes per token             */
+  SY_FAMILY_PER_QUERY = 3  /* batched op answered by one forward launch per query  */
+} sy_family;
+
+/* How a call will be executed: which kernel family and which compile-time tile.
+ * Pure host arithmetic on shapes -- no device is touched. */
+typedef struct sy_plan {
+  int32_t family;          /* sy_family                                          */
+  int32_t waves_per_token; /* wavefronts that share one token's D axis           */
+  int32_t chunks_per_lane; /* 16-byte chunks per lane per source row             */
+  int32_t rows_per_tile;   /* compile-time rows held in registers (NR)           */
+  int32_t elems_per_chunk; /* elements in one 16-byte chunk (8 for 16-bit types) */
+  int32_t block_threads;   /* threads per workgroup                              */
+  int32_t tokens_per_block;/* tokens a workgroup handles at once                 */
+  int32_t n_chunks;        /* softmax chunks per token (1 = resident)            */
+} sy_plan;
+
+/* Fill *out with the execution plan for op at the given shape. `aligned` says
+ * whether every pointer and row start is 16-byte aligned (the vector paths need
+ * it). Replaces the dispatch helpers _launch_config, _bwd_launch and
+ * _batched_launch (src/switchyard/triton_op.py:130-150, :267-276, :420-435). */
+int sy_plan_for(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_dtype,
+                int aligned, sy_plan* out);
+
+/* Forward of the autograd operator: out = AttnRes(v, w).
+ * Replaces _BlockAttnResTriton.forward and its _fwd_resident/_fwd_tiled
+ * launches (src/switchyard/triton_op.py:505-536, :50-117).
+ * `stats` may be NULL; when given it receives [2][N][n_tok] fp32: the logits,
+ * then the inverse RMS r_n, which sy_bwd can reuse instead of recomputing.
+ * w may have a different dtype from v (it is upcast, as in triton_op.py:67). */
+int sy_fwd(const void* v, const void* w, void* out, float* stats, int64_t n_src, int64_t n_tok,
+           int64_t d, int64_t src_stride, int v_dtype, int w_dtype, float eps, void* stream);
+
+/* Bytes of device workspace sy_bwd needs for this shape on the current device
+ * (per-workgroup fp32 dw partials). Returns < 0 (an sy_status) on bad input.
+ * Replaces the fp32 dw buffer of triton_op.py:550. */
+int64_t sy_bwd_workspace_bytes(int64_t n_src, int64_t n_tok, int64_t d, int v_dtype, int w_dtype);
+
+/* Backward of the autograd operator: dv (v dtype, contiguous [N][n_tok][D])
+ * and dw (w dtype, [D]) from grad_out (v dtype). dw is reduced
+ * deterministically (per-workgroup partials + fixed-order tree), with no float
+ * atomics. `stats` may be NULL (recompute) or the array sy_fwd wrote.
+ * Replaces _BlockAttnResTriton.backward with _bwd_resident and
+ * _bwd_stats/_bwd_apply (src/switchyard/triton_op.py:538-589, :194-375). */
+int sy_bwd(const void* v, const void* w, const void* grad_out, const float* stats, void* dv,
+           void* dw, void* workspace, int64_t workspace_bytes, int64_t n_src, int64_t n_tok,
+           int64_t d, int64_t src_stride, int v_dtype, int w_dtype, float eps, void* stream);
+
+/* Output-only batched forward: out[s] = AttnRes(v, queries[s]) for S queries
+ * sharing one read of v. queries has v's dtype.
+ * Replaces block_attn_res_batched/_fwd_batched_resident
+ * (src/switchyard/triton_op.py:438-501, :378-414). */
+int sy_fwd_batched(const void* v, const void* queries, void* out, int64_t n_src, int64_t n_q,
+                   int64_t n_tok, int64_t d, int64_t src_stride, int dtype, float eps,
+                   void* stream);
+
+/* Speed-of-light ceiling: out[t] = sum_n v_n[t] with the forward's geometry and
+ * bytes but no softmax. Replaces speed_of_light (src/switchyard/triton_op.py:153-191). */
+int sy_sol(const void* v, void* out, int64_t n_src, int64_t n_tok, int64_t d,
+           int64_t src_stride, int dtype, void* stream);
+
+/* HBM probes over `bytes` (a multiple of 16): kind 0 = read src (dst receives
+ * one float per workgroup, dst must hold sy_probe_grid(bytes) floats),
+ * 1 = write dst, 2 = copy src -> dst. Replaces the copy/read/write probes of
+ * bench/machine.py:41-61. */
+int sy_bw_probe(int kind, const void* src, void* dst, int64_t bytes, void* stream);
+int64_t sy_probe_grid(int64_t bytes);
+
+/* Static string for a status code (negative sy_status or positive hipError_t). */
+const char* sy_strerror(int code);
+
+/* SY_ABI_VERSION of the loaded library. */
+int sy_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SWITCHYARD_H */
