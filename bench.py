@@ -1,0 +1,463 @@
+#!/usr/bin/env python3
+"""Block AttnRes on one MI355X: fwd and fwd+bwd time and HBM roofline fraction.
+
+Workload (the one its metric is quoted on): N=9
+sources, B=1, T=4096, D=2048, bf16; v ~ N(0,1), w ~ N(0, 0.5) (std 0.5),
+grad_out ~ N(0,1), eps 1e-6. Inputs are generated on the CPU (seed 0),
+rounded to bf16 and copied to HBM before anything is timed.
+
+A *step* is one forward + backward of the operator on one batch: sy_fwd
+(1 kernel) then sy_bwd (2 kernels: the persistent backward and the dw
+reduction), called through the C ABI on torch's current stream. The timed
+region is exactly ``--steps`` steps between two synchronizes, cycling through
+``--rotations`` independent input/output sets (6 x 330 MiB, far beyond the
+256 MiB Infinity Cache) so no step finds its operands cached.
+
+``value`` = algorithmic fwd+bwd bytes ((3N+2) slabs of B*T*D*2 bytes) per
+second over the timed region, whole job (one GPU). ``roofline`` is for the
+dominant kernel (the backward: (2N+1) slabs per launch), timed live over
+``--steps`` back-to-back launches with HIP events on the launch stream.
+``cpu_baseline`` times the oracle's eager fp32 formulation (forward +
+backward through torch.autograd) on the host cores.
+
+Modes:
+  python bench.py [--steps K --warmup W]        the JSON line (stdout)
+  python bench.py --kernel {fwd,bwd,reduce,sol,copy} --iters K
+                                                run one kernel K times (for rocprofv3)
+  python bench.py --summarize DIR --title T     rocprofv3 CSV -> markdown summary
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+for _p in (ROOT / "blackwell-switchyard_amd", ROOT):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "fwd & fwd+bwd ms + % HBM roofline, N=9 B=1 T=4096 D=2048 bf16"
+HBM_PEAK_GBPS = 8000.0
+TRAFFIC_FILE = ROOT / "profiles" / "traffic_N9_B1_T4096_D2048_bf16.json"
+
+
+def log(*a) -> None:
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse_args() -> argparse.Namespace:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--n", type=int, default=9)
+    ap.add_argument("--b", type=int, default=1)
+    ap.add_argument("--t", type=int, default=4096)
+    ap.add_argument("--d", type=int, default=2048)
+    ap.add_argument("--dtype", default="bfloat16", choices=["bfloat16", "float16", "float32"])
+    ap.add_argument("--w-std", type=float, default=0.5, help="w ~ N(0, w_std); BASELINE.json uses 0.5")
+    ap.add_argument("--rotations", type=int, default=6)
+    ap.add_argument("--flushed-reps", type=int, default=50, help="reference-style per-rep flushed latency reps")
+    ap.add_argument("--cpu-budget-s", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="skip flushed latency, kernel count, memory")
+    ap.add_argument("--kernel", choices=["fwd", "bwd", "reduce", "sol", "copy"], default=None)
+    ap.add_argument("--iters", type=int, default=20)
+    ap.add_argument("--summarize", type=pathlib.Path, default=None)
+    ap.add_argument("--title", default="")
+    ap.add_argument("--json-out", type=pathlib.Path, default=None)
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------------------
+# Workload
+# ---------------------------------------------------------------------------
+
+
+class Workload:
+    """Rotating HBM-resident input/output sets and C-ABI step closures."""
+
+    def __init__(self, args, torch, device):
+        from switchyard import _lib
+
+        self.torch, self.dev, self.lib, self._lib = torch, device, _lib.lib(), _lib
+        self.n, self.b, self.t, self.d = args.n, args.b, args.t, args.d
+        self.dtype = getattr(torch, args.dtype)
+        self.n_tok = self.b * self.t
+        self.item = torch.finfo(self.dtype).bits // 8
+        self.slab = self.n_tok * self.d * self.item
+        gen = torch.Generator().manual_seed(0)
+        v = torch.randn(self.n, self.b, self.t, self.d, generator=gen).to(self.dtype)
+        w = (args.w_std * torch.randn(self.d, generator=gen)).to(self.dtype)
+        g = torch.randn(self.b, self.t, self.d, generator=gen).to(self.dtype)
+        self.cpu = (v, w, g)
+        self.w = w.to(device)
+        vt, gt = v.to(device), g.to(device)
+        self.code = _lib.dtype_code(self.dtype)
+        self.ws_bytes = int(self.lib.sy_bwd_workspace_bytes(self.n, self.n_tok, self.d, self.code, self.code))
+        self.rows = int(self.lib.sy_bwd_partial_rows(self.n, self.n_tok, self.d, self.code, self.code, 1, 1))
+        self.sets = []
+        for k in range(max(1, args.rotations)):
+            s = {
+                "v": vt if k == 0 else vt.clone(),
+                "g": gt if k == 0 else gt.clone(),
+                "out": torch.empty(self.b, self.t, self.d, device=device, dtype=self.dtype),
+                "stats": torch.empty(2, self.n, self.n_tok, device=device, dtype=torch.float32),
+                "dv": torch.empty(self.n, self.b, self.t, self.d, device=device, dtype=self.dtype),
+                "dw": torch.empty(self.d, device=device, dtype=self.dtype),
+                "ws": torch.empty(max(1, self.ws_bytes // 4), device=device, dtype=torch.float32),
+                "sol": torch.empty(self.b, self.t, self.d, device=device, dtype=self.dtype),
+            }
+            self.sets.append(s)
+        self.stream = _lib.stream_ptr(device)
+
+    @staticmethod
+    def _p(t):
+        return ctypes.c_void_p(t.data_ptr())
+
+    def _check(self, rc, what):
+        self._lib.check(rc, what)
+
+    def fwd(self, s):
+        self._check(self.lib.sy_fwd(self._p(s["v"]), self._p(self.w), self._p(s["out"]), self._p(s["stats"]),
+                                    self.n, self.n_tok, self.d, self.n_tok * self.d, self.code, self.code,
+                                    1e-6, self.stream), "sy_fwd")
+
+    def bwd(self, s):
+        self._check(self.lib.sy_bwd(self._p(s["v"]), self._p(self.w), self._p(s["g"]), self._p(s["stats"]),
+                                    self._p(s["dv"]), self._p(s["dw"]), self._p(s["ws"]), self.ws_bytes,
+                                    self.n, self.n_tok, self.d, self.n_tok * self.d, self.code, self.code,
+                                    1e-6, self.stream), "sy_bwd")
+
+    def bwd_main(self, s):
+        self._check(self.lib.sy_bwd_main(self._p(s["v"]), self._p(self.w), self._p(s["g"]), self._p(s["stats"]),
+                                         self._p(s["dv"]), self._p(s["ws"]), self.ws_bytes, self.n, self.n_tok,
+                                         self.d, self.n_tok * self.d, self.code, self.code, 1e-6, self.stream),
+                    "sy_bwd_main")
+
+    def reduce(self, s):
+        self._check(self.lib.sy_dw_reduce(self._p(s["ws"]), self.rows, self.d, self._p(s["dw"]), self.code,
+                                          self.stream), "sy_dw_reduce")
+
+    def sol(self, s):
+        self._check(self.lib.sy_sol(self._p(s["v"]), self._p(s["sol"]), self.n, self.n_tok, self.d,
+                                    self.n_tok * self.d, self.code, self.stream), "sy_sol")
+
+    def step(self, s):
+        self.fwd(s)
+        self.bwd(s)
+
+    def closures(self, name):
+        f = getattr(self, name)
+        return [(lambda s=s: f(s)) for s in self.sets]
+
+
+# ---------------------------------------------------------------------------
+# Reference-style extras (flushed per-rep latency, kernel counts, workspace)
+# ---------------------------------------------------------------------------
+
+
+def api_extras(wl, args, torch, harness):
+    from switchyard.hip_op import block_attn_res_hip, speed_of_light
+
+    dev = wl.dev
+    v = wl.sets[0]["v"]
+    vg = v.detach().clone().requires_grad_(True)
+    wg = wl.w.detach().clone().requires_grad_(True)
+    g = wl.sets[0]["g"]
+
+    def fwd():
+        return block_attn_res_hip(v, wl.w)
+
+    def fwd_bwd():
+        vg.grad = None
+        wg.grad = None
+        block_attn_res_hip(vg, wg).backward(g)
+
+    reps = args.flushed_reps
+    out = {
+        "method": "autograd API, caches flushed (1 GiB write) before every rep, HIP events, median",
+        "fwd": harness.measure_latency(fwd, device=dev, warmup=10, reps=reps).as_dict(),
+        "fwd_bwd": harness.measure_latency(fwd_bwd, device=dev, warmup=10, reps=reps).as_dict(),
+        "sol": harness.measure_latency(lambda: speed_of_light(v), device=dev, warmup=10, reps=reps).as_dict(),
+    }
+    try:
+        out["fwd_kernels"] = harness.count_kernels(fwd, device=dev).as_dict()
+        out["fwd_bwd_kernels"] = harness.count_kernels(fwd_bwd, device=dev).as_dict()
+    except Exception as exc:  # noqa: BLE001
+        out["kernel_count_error"] = str(exc)[:200]
+    resident = v.numel() * v.element_size() + wl.w.numel() * wl.w.element_size() + wl.slab
+    out["fwd_memory"] = harness.measure_memory(fwd, device=dev, resident_bytes=resident).as_dict()
+    out["fwd_bwd_memory"] = harness.measure_memory(fwd_bwd, device=dev, resident_bytes=resident,
+                                                    output_bytes=wl.slab).as_dict()
+    return out
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline leg: the only part of bench.py that touches oracle/
+# ---------------------------------------------------------------------------
+
+
+def cpu_baseline_leg(wl, args, torch):
+    """Time the oracle's eager fp32 formulation on the host and, as the
+    checker, compare a 512-token slice of the GPU op with the float64 oracle."""
+    from oracle import reference as oref
+    from switchyard.hip_op import block_attn_res_hip
+
+    v, w, g = wl.cpu
+    # -- checker: GPU op on a token slice vs float64 oracle -------------------
+    ts = min(512, wl.t)
+    vs, gs = v[:, :, :ts].contiguous(), g[:, :ts].contiguous()
+    vt = vs.to(wl.dev).requires_grad_(True)
+    wt = w.to(wl.dev).requires_grad_(True)
+    out = block_attn_res_hip(vt, wt)
+    out.backward(gs.to(wl.dev))
+    o64 = oref.block_attn_res_oracle(vs, w)
+    dv64, dw64 = oref.oracle_grads(vs, w, gs)
+    check = {}
+    for name, got, ref in (("out", out, o64), ("dv", vt.grad, dv64), ("dw", wt.grad, dw64)):
+        err, floor = oref.rel_l2(got, ref), oref.dtype_floor(ref, wl.dtype)
+        check[name] = {"rel_l2": err, "floor": floor, "ratio": err / floor if floor else None}
+    # Token independence: the slice's output equals the full run's first tokens.
+    full = wl.sets[0]["out"][:, :ts].cpu()
+    check["slice_matches_full_run"] = bool(torch.equal(out.detach().cpu(), full))
+    check["ok"] = all(check[k]["ratio"] is not None and check[k]["ratio"] <= 1.10 for k in ("out", "dv", "dw"))
+
+    # -- timed CPU baseline ---------------------------------------------------
+    threads = torch.get_num_threads()
+    v32 = v.float().requires_grad_(True)
+    w32 = w.float().requires_grad_(True)
+    g32 = g.float()
+
+    def once():
+        v32.grad = None
+        w32.grad = None
+        oref.folded_form(v32, w32, oref.DEFAULT_EPS).backward(g32)
+
+    t0 = time.perf_counter()
+    once()  # warmup, also sizes the rep count
+    first = time.perf_counter() - t0
+    reps = max(1, min(5, int(args.cpu_budget_s / max(first, 1e-3))))
+    samples = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        once()
+        samples.append(time.perf_counter() - t0)
+    samples.sort()
+    med = samples[len(samples) // 2]
+    nbytes = (3 * wl.n + 2) * wl.slab
+    cpu = {
+        "value": nbytes / med / 1e9,
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"full workload (N={wl.n} B={wl.b} T={wl.t} D={wl.d}), fp32 copies of the bf16 inputs; "
+                   f"oracle.reference.folded_form forward + torch.autograd backward; median of {reps} reps "
+                   f"after 1 warmup; {med * 1e3:.1f} ms per fwd+bwd"),
+        "ms_per_step": med * 1e3,
+        "host_cpu": None,
+    }
+    return check, cpu
+
+
+# ---------------------------------------------------------------------------
+# Modes
+# ---------------------------------------------------------------------------
+
+
+def run_kernel_mode(args):
+    """Launch one kernel --iters times over the rotating sets (rocprofv3 target)."""
+    import torch
+
+    from switchyard import harness
+    from switchyard.hip_op import bandwidth_probe
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    if args.kernel == "copy":
+        nbytes = 1 << 30
+        src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(3)
+        dst = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        for _ in range(args.iters):
+            bandwidth_probe("copy", src, dst)
+        torch.cuda.synchronize(dev)
+        log(f"copy probe: {args.iters} x {nbytes} bytes")
+        return
+    wl = Workload(args, torch, dev)
+    for s in wl.sets:  # stats/partials must exist for bwd/reduce
+        wl.fwd(s)
+        if args.kernel == "reduce":
+            wl.bwd_main(s)
+    torch.cuda.synchronize(dev)
+    name = {"fwd": "fwd", "bwd": "bwd_main", "reduce": "reduce", "sol": "sol"}[args.kernel]
+    fns = wl.closures(name)
+    ms = harness.time_loop(fns, device=dev, iters=args.iters)
+    log(f"{args.kernel}: {args.iters} launches, {ms * 1e3:.2f} us average (HIP events)")
+
+
+def summarize(args):
+    """Condense rocprofv3 CSV output under DIR into a short markdown table."""
+    import csv
+
+    d = args.summarize
+    stats = sorted(d.rglob("*kernel_stats.csv"))
+    counters = sorted(d.rglob("*counter_collection.csv"))
+    lines = [f"### {args.title or d.name}", ""]
+    for f in stats:
+        lines += ["| kernel | calls | avg us | min us | max us |", "|---|---:|---:|---:|---:|"]
+        with open(f) as fh:
+            for row in csv.DictReader(fh):
+                name = row.get("Name") or row.get("KernelName") or "?"
+                lines.append(f"| `{name[:90]}` | {row.get('Calls')} | {float(row.get('AverageNs', 0)) / 1e3:.2f} | "
+                             f"{float(row.get('MinNs', 0)) / 1e3:.2f} | {float(row.get('MaxNs', 0)) / 1e3:.2f} |")
+        lines.append("")
+    for f in counters:
+        agg: dict[tuple[str, str], list[float]] = {}
+        with open(f) as fh:
+            for row in csv.DictReader(fh):
+                key = ((row.get("Kernel_Name") or "?")[:90], row.get("Counter_Name") or "?")
+                agg.setdefault(key, []).append(float(row.get("Counter_Value") or 0))
+        lines += ["| kernel | counter | dispatches | mean per dispatch |", "|---|---|---:|---:|"]
+        for (k, c), vals in sorted(agg.items()):
+            lines.append(f"| `{k}` | {c} | {len(vals)} | {sum(vals) / len(vals):.1f} |")
+        lines.append("")
+    print("\n".join(lines))
+
+
+def main() -> None:
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus > 1 or world > 1:
+        print("bench.py: this build measures one GPU only (the operator is independent per token; "
+              "see DESIGN.md for how it shards). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    if args.summarize is not None:
+        summarize(args)
+        return
+    if args.kernel is not None:
+        run_kernel_mode(args)
+        return
+
+    import torch
+
+    from switchyard import harness
+    from switchyard.reference import attn_res_min_bytes, attn_res_train_bytes
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    wl = Workload(args, torch, dev)
+    n, b, t, d, item = wl.n, wl.b, wl.t, wl.d, wl.item
+    fwd_bytes = attn_res_min_bytes(n, b, t, d, item)
+    step_bytes = attn_res_train_bytes(n, b, t, d, item)
+    bwd_bytes = (2 * n + 1) * wl.slab
+    sol_bytes = fwd_bytes
+
+    steps = [(lambda s=s: wl.step(s)) for s in wl.sets]
+    for i in range(args.warmup):
+        steps[i % len(steps)]()
+    torch.cuda.synchronize(dev)
+
+    # ---- timed region: exactly --steps steps ------------------------------
+    t0 = time.perf_counter()
+    ms_step = harness.time_loop(steps, device=dev, iters=args.steps)
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    log(f"step (fwd+bwd): {ms_step * 1e3:.2f} us  [{step_bytes / ms_step / 1e6:.0f} GB/s]  wall {wall_ms * 1e3:.2f} us")
+
+    # ---- per-kernel averages, live, HIP events on the launch stream --------
+    k_iters = max(args.steps, 50)
+    per = {}
+    for name in ("fwd", "bwd_main", "reduce", "sol"):
+        per[name] = harness.time_loop(wl.closures(name), device=dev, iters=k_iters)
+    nbytes_copy = 1 << 30
+    src = torch.empty(nbytes_copy, dtype=torch.uint8, device=dev).fill_(3)
+    dst = torch.empty(nbytes_copy, dtype=torch.uint8, device=dev)
+    from switchyard.hip_op import bandwidth_probe
+
+    copy_ms = harness.time_loop([lambda: bandwidth_probe("copy", src, dst)], device=dev, iters=20)
+    copy_gbps = 2 * nbytes_copy / copy_ms / 1e6
+    del src, dst
+    for k, ms in per.items():
+        log(f"  {k:9s} {ms * 1e3:8.2f} us")
+    log(f"  copy probe {copy_gbps:.0f} GB/s (read+write)")
+
+    fwd_gbps = fwd_bytes / per["fwd"] / 1e6
+    bwd_gbps = bwd_bytes / per["bwd_main"] / 1e6
+    traffic = None
+    if TRAFFIC_FILE.exists() and (n, b, t, d, args.dtype) == (9, 1, 4096, 2048, "bfloat16"):
+        try:
+            traffic = json.loads(TRAFFIC_FILE.read_text()).get("bwd_main_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+
+    rec = {
+        "metric": METRIC,
+        "value": round(step_bytes / ms_step / 1e6, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {"bfloat16": "bf16", "float16": "f16", "float32": "f32"}[args.dtype],
+        "data": f"synthetic, CPU seed 0: v~N(0,1), w~N(0,{args.w_std}), grad_out~N(0,1), rounded to {args.dtype}",
+        "config": {"workload": "Block AttnRes fwd+bwd (sy_fwd + sy_bwd via the C ABI)", "n_src": n, "batch": b,
+                   "seq_len": t, "d_model": d, "eps": 1e-6, "parallelism": "none (1 GPU)",
+                   "rotating_sets": len(wl.sets)},
+        "roofline": {
+            "kernel": "k_bwd (persistent backward: reads v and grad_out, writes dv)",
+            "bound": "hbm",
+            "achieved": round(bwd_gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(bwd_gbps / HBM_PEAK_GBPS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes_per_launch": bwd_bytes,
+            "avg_launch_us": round(per["bwd_main"] * 1e3, 3),
+        },
+        "fwd": {"kernel": "k_fwd", "avg_launch_us": round(per["fwd"] * 1e3, 3), "bytes": fwd_bytes,
+                "achieved_gbps": round(fwd_gbps, 1), "frac_hbm_peak": round(fwd_gbps / HBM_PEAK_GBPS, 4),
+                "frac_of_sol_kernel": round(per["sol"] / per["fwd"], 4),
+                "frac_of_copy_probe": round(fwd_gbps / copy_gbps, 4)},
+        "fwd_bwd": {"ms": round(ms_step, 5), "bytes": step_bytes, "achieved_gbps": round(step_bytes / ms_step / 1e6, 1),
+                    "frac_hbm_peak": round(step_bytes / ms_step / 1e6 / HBM_PEAK_GBPS, 4),
+                    "kernels_per_step": 3, "wall_ms_per_step": round(wall_ms, 5)},
+        "kernels_us": {k: round(v * 1e3, 3) for k, v in per.items()},
+        "sol_gbps": round(sol_bytes / per["sol"] / 1e6, 1),
+        "copy_probe_gbps": round(copy_gbps, 1),
+        "bwd_workspace_bytes": wl.ws_bytes,
+        "stats_bytes": 2 * n * wl.n_tok * 4,
+    }
+    if not args.no_extras:
+        try:
+            rec["reference_method"] = api_extras(wl, args, torch, harness)
+        except Exception as exc:  # noqa: BLE001
+            rec["reference_method"] = {"error": f"{type(exc).__name__}: {exc}"[:300]}
+    rec["cpu_baseline"] = None
+    if not args.no_cpu_baseline:
+        try:
+            check, cpu = cpu_baseline_leg(wl, args, torch)
+            cpu["host_cpu"] = harness.cpu_model()
+            rec["cpu_baseline"] = cpu
+            rec["correctness"] = check
+        except Exception as exc:  # noqa: BLE001
+            rec["cpu_baseline_error"] = f"{type(exc).__name__}: {exc}"[:300]
+    rec["environment"] = harness.environment()
+    rec["commit"] = harness.repository_commit(str(ROOT))
+    line = json.dumps(rec)
+    if args.json_out:
+        args.json_out.parent.mkdir(parents=True, exist_ok=True)
+        args.json_out.write_text(line + "\n")
+    print(line, flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -2,9 +2,9 @@
 // Every check that can be made on the host is made before any device work,
 // so bad arguments come back as negative sy_status codes. Nothing here
 // allocates device memory.
+#include <cstdlib>
 #include <map>
 #include <mutex>
-#include <tuple>
 
 #include "../../include/switchyard.h"
 #include "sy_launch.hpp"
@@ -26,49 +26,31 @@ int status(hipError_t e) { return e == hipSuccess ? SY_OK : (int)e; }
 
 std::mutex g_mu;
 std::map<int, int> g_cus;                                   // device -> CU count
-std::map<std::tuple<int, int, int, int, int>, int> g_occ;   // (dev,dtype,W,VPL,NR) -> blocks/CU
 
-hipError_t current_device(int* dev) { return hipGetDevice(dev); }
-
-hipError_t bwd_blocks_per_cu(const sy_plan& p, int dtype, int* out) {
-  int dev = 0;
-  hipError_t e = current_device(&dev);
-  if (e != hipSuccess) return e;
-  const auto key = std::make_tuple(dev, dtype, p.waves_per_token, p.chunks_per_lane, p.rows_per_tile);
-  {
-    std::lock_guard<std::mutex> lk(g_mu);
-    auto it = g_occ.find(key);
-    if (it != g_occ.end()) {
-      *out = it->second;
-      return hipSuccess;
-    }
-  }
-  int n = 0;
-  if (dtype == SY_BF16) {
-    e = bwd_vec_blocks_per_cu_bf16(p, &n);
-  } else if (dtype == SY_F16) {
-    e = bwd_vec_blocks_per_cu_f16(p, &n);
-  } else {
-    e = bwd_vec_blocks_per_cu_f32(p, &n);
-  }
-  if (e != hipSuccess) return e;
-  if (n < 1) n = 1;
-  std::lock_guard<std::mutex> lk(g_mu);
-  g_occ[key] = n;
-  *out = n;
-  return hipSuccess;
+hipError_t bwd_resources(const sy_plan& p, int dtype, bool stats, KernelRes* out) {
+  if (dtype == SY_BF16) return bwd_vec_resources_bf16(p, stats, out);
+  if (dtype == SY_F16) return bwd_vec_resources_f16(p, stats, out);
+  return bwd_vec_resources_f32(p, stats, out);
 }
 
-// Persistent workgroup count of the backward: enough to fill every CU at the
-// kernel's occupancy, never more than there are token slots.
-int bwd_grid(const sy_plan& p, int64_t n_tok, int dtype, int* grid) {
+// Persistent workgroup count of the backward: every CU filled at the
+// kernel's register/LDS occupancy, never more than there are token slots.
+// Deterministic in (plan, n_tok, stats, device), which keeps dw bit-stable.
+int bwd_grid(const sy_plan& p, int64_t n_tok, int dtype, bool stats, int* grid) {
   int cus = 0;
   hipError_t e = cu_count(&cus);
   if (e != hipSuccess) return e == hipErrorNoDevice ? SY_ERR_DEVICE : (int)e;
   int per_cu = 4;
   if (p.family != SY_FAMILY_GENERIC) {
-    e = bwd_blocks_per_cu(p, dtype, &per_cu);
+    KernelRes r;
+    e = bwd_resources(p, dtype, stats, &r);
     if (e != hipSuccess) return (int)e;
+    per_cu = r.blocks_per_cu;
+  }
+  // Tuning knob for measurement sweeps: workgroups per CU of the persistent grid.
+  if (const char* env = std::getenv("SY_BWD_BLOCKS_PER_CU")) {
+    const int k = std::atoi(env);
+    if (k >= 1 && k <= 64) per_cu = k;
   }
   const int64_t slots = (n_tok + p.tokens_per_block - 1) / p.tokens_per_block;
   int64_t g = (int64_t)cus * per_cu;
@@ -79,9 +61,9 @@ int bwd_grid(const sy_plan& p, int64_t n_tok, int dtype, int* grid) {
 }
 
 hipError_t fwd_vec(const sy_plan& p, const FwdArgs& a, hipStream_t s) {
-  if (a.v_dtype == SY_BF16) return launch_fwd_vec_bf16(p, a, s);
-  if (a.v_dtype == SY_F16) return launch_fwd_vec_f16(p, a, s);
-  return launch_fwd_vec_f32(p, a, s);
+  if (a.v_dtype == SY_BF16) return launch_fwd_vec_bf16(p, a, s, nullptr);
+  if (a.v_dtype == SY_F16) return launch_fwd_vec_f16(p, a, s, nullptr);
+  return launch_fwd_vec_f32(p, a, s, nullptr);
 }
 hipError_t sol_vec(const sy_plan& p, const FwdArgs& a, hipStream_t s) {
   if (a.v_dtype == SY_BF16) return launch_sol_vec_bf16(p, a, s);
@@ -192,26 +174,29 @@ int64_t sy_bwd_workspace_bytes(int64_t n_src, int64_t n_tok, int64_t d, int v_dt
   apply_tile_override(SY_OP_BWD, n_src, d, &pv);
   rc = make_plan(SY_OP_BWD, n_src, 0, d, v_dtype, w_dtype, 0, &pg);
   if (rc != SY_OK) return rc;
-  int g1 = 0, g2 = 0;
-  rc = bwd_grid(pv, n_tok, v_dtype, &g1);
-  if (rc != SY_OK) return rc;
-  rc = bwd_grid(pg, n_tok, v_dtype, &g2);
-  if (rc != SY_OK) return rc;
-  const int64_t g = g1 > g2 ? g1 : g2;
+  int64_t g = 0;
+  for (const sy_plan* pp : {&pv, &pg}) {
+    for (bool st : {true, false}) {
+      int gi = 0;
+      rc = bwd_grid(*pp, n_tok, v_dtype, st, &gi);
+      if (rc != SY_OK) return rc;
+      if (gi > g) g = gi;
+    }
+  }
   return g * d * (int64_t)sizeof(float);
 }
 
-int sy_bwd(const void* v, const void* w, const void* grad_out, const float* stats, void* dv,
-           void* dw, void* workspace, int64_t workspace_bytes, int64_t n_src, int64_t n_tok,
-           int64_t d, int64_t src_stride, int v_dtype, int w_dtype, float eps, void* stream) {
-  // dw is written even when there are no tokens (it is then zero).
-  if (dw == nullptr) return SY_ERR_NULL;
+// Main backward kernel: dv and the fp32 dw partials. *rows_out receives the
+// partial row count (the persistent grid).
+static int bwd_main(const void* v, const void* w, const void* grad_out, const float* stats,
+                    void* dv, void* workspace, int64_t workspace_bytes, int64_t n_src,
+                    int64_t n_tok, int64_t d, int64_t src_stride, int v_dtype, int w_dtype,
+                    float eps, hipStream_t s, int* rows_out) {
+  *rows_out = 0;
   if (n_tok != 0 && (v == nullptr || w == nullptr || grad_out == nullptr || dv == nullptr))
     return SY_ERR_NULL;
   int rc = check_common(n_src, n_tok, d, src_stride, v_dtype, w_dtype);
-  if (rc != SY_OK) return rc;
-  const hipStream_t s = (hipStream_t)stream;
-  if (n_tok == 0) return status(launch_dw_reduce(nullptr, 0, (int)d, dw, w_dtype, s));
+  if (rc != SY_OK || n_tok == 0) return rc;
   const bool aligned = rows_aligned(v, src_stride, v_dtype) && rows_aligned(v, d, v_dtype) &&
                        al16(w) && al16(grad_out) && al16(dv) && al16(workspace) &&
                        (d * esize(v_dtype)) % 16 == 0;
@@ -220,16 +205,95 @@ int sy_bwd(const void* v, const void* w, const void* grad_out, const float* stat
   if (rc != SY_OK) return rc;
   apply_tile_override(SY_OP_BWD, n_src, d, &p);
   int grid = 0;
-  rc = bwd_grid(p, n_tok, v_dtype, &grid);
+  rc = bwd_grid(p, n_tok, v_dtype, stats != nullptr, &grid);
   if (rc != SY_OK) return rc;
   if (workspace == nullptr || workspace_bytes < (int64_t)grid * d * (int64_t)sizeof(float))
     return SY_ERR_WORKSPACE;
-  const BwdArgs a{v, w, grad_out, stats, dv, dw, (float*)workspace, (int)n_src, n_tok, (int)d,
+  const BwdArgs a{v, w, grad_out, stats, dv, nullptr, (float*)workspace, (int)n_src, n_tok, (int)d,
                   src_stride, v_dtype, w_dtype, eps};
   hipError_t e = p.family == SY_FAMILY_GENERIC ? launch_bwd_generic(a, grid, s)
                                                : bwd_vec(p, a, grid, s);
   if (e != hipSuccess) return (int)e;
-  return status(launch_dw_reduce((const float*)workspace, grid, (int)d, dw, w_dtype, s));
+  *rows_out = grid;
+  return SY_OK;
+}
+
+int sy_bwd(const void* v, const void* w, const void* grad_out, const float* stats, void* dv,
+           void* dw, void* workspace, int64_t workspace_bytes, int64_t n_src, int64_t n_tok,
+           int64_t d, int64_t src_stride, int v_dtype, int w_dtype, float eps, void* stream) {
+  // dw is written even when there are no tokens (it is then zero).
+  if (dw == nullptr) return SY_ERR_NULL;
+  const hipStream_t s = (hipStream_t)stream;
+  int rows = 0;
+  const int rc = bwd_main(v, w, grad_out, stats, dv, workspace, workspace_bytes, n_src, n_tok, d,
+                          src_stride, v_dtype, w_dtype, eps, s, &rows);
+  if (rc != SY_OK) return rc;
+  return status(launch_dw_reduce((const float*)workspace, rows, (int)d, dw, w_dtype, s));
+}
+
+int sy_bwd_main(const void* v, const void* w, const void* grad_out, const float* stats, void* dv,
+                void* workspace, int64_t workspace_bytes, int64_t n_src, int64_t n_tok, int64_t d,
+                int64_t src_stride, int v_dtype, int w_dtype, float eps, void* stream) {
+  int rows = 0;
+  return bwd_main(v, w, grad_out, stats, dv, workspace, workspace_bytes, n_src, n_tok, d,
+                  src_stride, v_dtype, w_dtype, eps, (hipStream_t)stream, &rows);
+}
+
+int64_t sy_bwd_partial_rows(int64_t n_src, int64_t n_tok, int64_t d, int v_dtype, int w_dtype,
+                            int aligned, int has_stats) {
+  int rc = check_common(n_src, n_tok, d, n_tok * d, v_dtype, w_dtype);
+  if (rc != SY_OK) return rc;
+  if (n_tok == 0) return 0;
+  sy_plan p;
+  rc = make_plan(SY_OP_BWD, n_src, 0, d, v_dtype, w_dtype, aligned, &p);
+  if (rc != SY_OK) return rc;
+  apply_tile_override(SY_OP_BWD, n_src, d, &p);
+  int grid = 0;
+  rc = bwd_grid(p, n_tok, v_dtype, has_stats != 0, &grid);
+  return rc != SY_OK ? rc : grid;
+}
+
+int sy_kernel_info(int op, int64_t n_src, int64_t n_tok, int64_t d, int v_dtype, int w_dtype,
+                   int32_t out[4]) {
+  if (out == nullptr) return SY_ERR_NULL;
+  int rc = check_common(n_src, n_tok, d, n_tok * d, v_dtype, w_dtype);
+  if (rc != SY_OK) return rc;
+  if (op != SY_OP_FWD && op != SY_OP_BWD) return SY_ERR_OP;
+  sy_plan p;
+  rc = make_plan(op, n_src, 0, d, v_dtype, w_dtype, 1, &p);
+  if (rc != SY_OK) return rc;
+  apply_tile_override(op, n_src, d, &p);
+  out[0] = out[1] = out[2] = out[3] = 0;
+  if (p.family == SY_FAMILY_GENERIC) return SY_OK;
+  KernelRes r{0, 0, 0, 0};
+  hipError_t e;
+  if (op == SY_OP_FWD) {
+    const FwdArgs a{nullptr, nullptr, nullptr, nullptr, (int)n_src, n_tok, (int)d, n_tok * d,
+                    v_dtype, w_dtype, 0.0f};
+    e = v_dtype == SY_BF16 ? launch_fwd_vec_bf16(p, a, nullptr, &r)
+        : v_dtype == SY_F16 ? launch_fwd_vec_f16(p, a, nullptr, &r)
+                            : launch_fwd_vec_f32(p, a, nullptr, &r);
+  } else {
+    e = bwd_resources(p, v_dtype, true, &r);
+    if (e == hipSuccess) {
+      rc = bwd_grid(p, n_tok, v_dtype, true, &r.grid);
+      if (rc != SY_OK) return rc;
+    }
+  }
+  if (e != hipSuccess) return e == hipErrorNoDevice ? SY_ERR_DEVICE : (int)e;
+  out[0] = r.vgprs;
+  out[1] = r.lds;
+  out[2] = r.blocks_per_cu;
+  out[3] = r.grid;
+  return SY_OK;
+}
+
+int sy_dw_reduce(const float* partial, int64_t rows, int64_t d, void* dw, int w_dtype,
+                 void* stream) {
+  if (dw == nullptr || (rows > 0 && partial == nullptr)) return SY_ERR_NULL;
+  if (!valid_dtype(w_dtype)) return SY_ERR_DTYPE;
+  if (rows < 0 || rows > 0x7fffffff || d < 1 || d > 0x7fffffff / 16) return SY_ERR_SHAPE;
+  return status(launch_dw_reduce(partial, (int)rows, (int)d, dw, w_dtype, (hipStream_t)stream));
 }
 
 int sy_fwd_batched(const void* v, const void* queries, void* out, int64_t n_src, int64_t n_q,

@@ -33,11 +33,27 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint3
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kRsrcFlags);
 }
 
+// Cache policy of streamed traffic (v, grad_out in; out, dv out): every byte
+// is touched once, so the loads carry the `nt` (non-temporal) hint by default.
+// Operands every wave re-reads (w, queries) use the default policy.
+#ifndef SY_STREAM_LOAD_AUX
+#define SY_STREAM_LOAD_AUX 2
+#endif
+#ifndef SY_STREAM_STORE_AUX
+#define SY_STREAM_STORE_AUX 2
+#endif
+
 __device__ __forceinline__ i32x4_t ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
 }
+__device__ __forceinline__ i32x4_t ld16_stream(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, SY_STREAM_LOAD_AUX);
+}
 __device__ __forceinline__ void st16(__amdgpu_buffer_rsrc_t r, uint32_t off, i32x4_t x) {
   __builtin_amdgcn_raw_buffer_store_b128(x, r, off, 0, 0);
+}
+__device__ __forceinline__ void st16_stream(__amdgpu_buffer_rsrc_t r, uint32_t off, i32x4_t x) {
+  __builtin_amdgcn_raw_buffer_store_b128(x, r, off, 0, SY_STREAM_STORE_AUX);
 }
 
 // ---------------------------------------------------------------- conversion

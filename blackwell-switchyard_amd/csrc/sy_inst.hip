@@ -1,5 +1,7 @@
 // Instantiates the register-tiled kernels for one dtype and maps a plan onto
 // them. Built three times: -DSY_TAG=BF16 -DSY_NAME=bf16, F16/f16, F32/f32.
+#include <algorithm>
+
 #include "sy_kernels.hpp"
 #include "sy_launch.hpp"
 
@@ -21,20 +23,65 @@ bool tile_is(const sy_plan& p, int w, int vpl, int nr) {
   return p.waves_per_token == w && p.chunks_per_lane == vpl && p.rows_per_tile == nr;
 }
 
-int64_t blocks_for(const sy_plan& p, int64_t n_tok) {
-  return (n_tok + p.tokens_per_block - 1) / p.tokens_per_block;
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Persistent grid = CUs x the workgroups one CU holds at this kernel's
+// register and LDS footprint (unified 512-entry VGPR file per SIMD lane, at
+// most 8 waves per SIMD, 160 KiB LDS per CU), capped by the token slots.
+int launch_grid(const KernelRes& res, int64_t n_tok, int tpb) {
+  int cus = 0;
+  if (cu_count(&cus) != hipSuccess || cus < 1) cus = 1;
+  const int64_t g = std::min<int64_t>((int64_t)cus * res.blocks_per_cu, cdiv(n_tok, tpb));
+  return (int)std::max<int64_t>(1, g);
+}
+
+template <class K>
+KernelRes resources_of(K* kernel, int block_threads) {
+  KernelRes r{0, 0, 1, 0};
+  hipFuncAttributes a;
+  if (hipFuncGetAttributes(&a, reinterpret_cast<const void*>(kernel)) != hipSuccess) return r;
+  r.vgprs = a.numRegs;
+  r.lds = (int)a.sharedSizeBytes;
+  const int alloc = std::max(8, ((a.numRegs + 7) / 8) * 8);
+  const int waves_simd = std::min(8, 512 / alloc);
+  const int by_waves = waves_simd * 4 / (block_threads / 64);
+  const int by_lds = r.lds > 0 ? (160 * 1024) / r.lds : 64;
+  r.blocks_per_cu = std::max(1, std::min(by_waves, by_lds));
+  return r;
 }
 }  // namespace
 
-hipError_t SY_FN(launch_fwd_vec_)(const sy_plan& p, const FwdArgs& a, hipStream_t s) {
+hipError_t SY_FN(launch_fwd_vec_)(const sy_plan& p, const FwdArgs& a, hipStream_t s,
+                                 KernelRes* info) {
   const float inv_d = 1.0f / (float)a.d;
-  const dim3 grid((unsigned)blocks_for(p, a.n_tok));
-#define X(W_, V_, N_)                                                                      \
-  if (tile_is(p, W_, V_, N_)) {                                                            \
-    hipLaunchKernelGGL((k_fwd<T, W_, V_, N_>), grid, dim3(FwdGeom<W_>::kBlock), 0, s,      \
-                       (const St*)a.v, (const St*)a.w, (St*)a.out, a.stats, a.n_src, a.n_tok, \
-                       a.d, a.src_stride, a.eps, inv_d);                                   \
-    return hipGetLastError();                                                              \
+  const bool res = p.family == SY_FAMILY_RESIDENT;
+#define X(W_, V_, N_)                                                                           \
+  if (tile_is(p, W_, V_, N_)) {                                                                 \
+    constexpr int kB = FwdGeom<W_>::kBlock, kT = FwdGeom<W_>::kTpb;                             \
+    if (res) {                                                                                  \
+      static const KernelRes kr = resources_of(k_fwd_res<T, W_, V_, N_>, kB);                   \
+      const int grid = launch_grid(kr, a.n_tok, kT);                                            \
+      if (info) {                                                                               \
+        *info = kr;                                                                             \
+        info->grid = grid;                                                                      \
+        return hipSuccess;                                                                      \
+      }                                                                                         \
+      const int n_iter = (int)cdiv(a.n_tok, (int64_t)grid * kT);                                \
+      hipLaunchKernelGGL((k_fwd_res<T, W_, V_, N_>), dim3(grid), dim3(kB), 0, s, (const St*)a.v, \
+                         (const St*)a.w, (St*)a.out, a.stats, a.n_src, a.n_tok, a.d,             \
+                         a.src_stride, a.eps, inv_d, n_iter);                                   \
+    } else {                                                                                    \
+      const int64_t grid = cdiv(a.n_tok, kT);                                                   \
+      if (info) {                                                                               \
+        *info = resources_of(k_fwd<T, W_, V_, N_>, kB);                                         \
+        info->grid = (int)grid;                                                                 \
+        return hipSuccess;                                                                      \
+      }                                                                                         \
+      hipLaunchKernelGGL((k_fwd<T, W_, V_, N_>), dim3((unsigned)grid), dim3(kB), 0, s,          \
+                         (const St*)a.v, (const St*)a.w, (St*)a.out, a.stats, a.n_src, a.n_tok, \
+                         a.d, a.src_stride, a.eps, inv_d);                                      \
+    }                                                                                           \
+    return hipGetLastError();                                                                   \
   }
   SY_TILES(X)
 #undef X
@@ -42,12 +89,20 @@ hipError_t SY_FN(launch_fwd_vec_)(const sy_plan& p, const FwdArgs& a, hipStream_
 }
 
 hipError_t SY_FN(launch_sol_vec_)(const sy_plan& p, const FwdArgs& a, hipStream_t s) {
-  const dim3 grid((unsigned)blocks_for(p, a.n_tok));
-#define X(W_, V_, N_)                                                                       \
-  if (tile_is(p, W_, V_, N_)) {                                                             \
-    hipLaunchKernelGGL((k_sol<T, W_, V_, N_>), grid, dim3(FwdGeom<W_>::kBlock), 0, s,       \
-                       (const St*)a.v, (St*)a.out, a.n_src, a.n_tok, a.d, a.src_stride);     \
-    return hipGetLastError();                                                               \
+  const bool res = p.family == SY_FAMILY_RESIDENT;
+#define X(W_, V_, N_)                                                                          \
+  if (tile_is(p, W_, V_, N_)) {                                                                \
+    constexpr int kB = FwdGeom<W_>::kBlock, kT = FwdGeom<W_>::kTpb;                            \
+    if (res) {                                                                                 \
+      static const KernelRes kr = resources_of(k_sol_res<T, W_, V_, N_>, kB);                  \
+      hipLaunchKernelGGL((k_sol_res<T, W_, V_, N_>), dim3(launch_grid(kr, a.n_tok, kT)),       \
+                         dim3(kB), 0, s, (const St*)a.v, (St*)a.out, a.n_src, a.n_tok, a.d,     \
+                         a.src_stride);                                                        \
+    } else {                                                                                   \
+      hipLaunchKernelGGL((k_sol<T, W_, V_, N_>), dim3((unsigned)cdiv(a.n_tok, kT)), dim3(kB), 0, \
+                         s, (const St*)a.v, (St*)a.out, a.n_src, a.n_tok, a.d, a.src_stride);   \
+    }                                                                                          \
+    return hipGetLastError();                                                                  \
   }
   SY_TILES(X)
 #undef X
@@ -56,13 +111,29 @@ hipError_t SY_FN(launch_sol_vec_)(const sy_plan& p, const FwdArgs& a, hipStream_
 
 hipError_t SY_FN(launch_batched_vec_)(const sy_plan& p, const BatchedArgs& a, hipStream_t s) {
   const float inv_d = 1.0f / (float)a.d;
-  const dim3 grid((unsigned)blocks_for(p, a.n_tok));
-#define X(W_, V_, N_)                                                                          \
-  if (tile_is(p, W_, V_, N_)) {                                                                \
-    hipLaunchKernelGGL((k_batched<T, W_, V_, N_>), grid, dim3(FwdGeom<W_>::kBlock), 0, s,      \
-                       (const St*)a.v, (const St*)a.q, (St*)a.out, a.n_src, a.n_q, a.n_tok, a.d, \
-                       a.src_stride, a.eps, inv_d);                                            \
-    return hipGetLastError();                                                                  \
+#define X(W_, V_, N_)                                                                            \
+  if (tile_is(p, W_, V_, N_)) {                                                                  \
+    constexpr int kB = FwdGeom<W_>::kBlock, kT = FwdGeom<W_>::kTpb;                              \
+    hipLaunchKernelGGL((k_batched<T, W_, V_, N_>), dim3((unsigned)cdiv(a.n_tok, kT)), dim3(kB), 0, \
+                       s, (const St*)a.v, (const St*)a.q, (St*)a.out, a.n_src, a.n_q, a.n_tok,    \
+                       a.d, a.src_stride, a.eps, inv_d);                                         \
+    return hipGetLastError();                                                                    \
+  }
+  SY_TILES(X)
+#undef X
+  return hipErrorInvalidConfiguration;
+}
+
+// The backward's grid must be known before launch (it sizes the workspace),
+// so it is computed here from the instantiation's resources.
+hipError_t SY_FN(bwd_vec_resources_)(const sy_plan& p, bool stats, KernelRes* out) {
+#define X(W_, V_, N_)                                                                 \
+  if (tile_is(p, W_, V_, N_)) {                                                       \
+    constexpr int kB = BwdGeom<W_>::kBlock;                                           \
+    static const KernelRes with = resources_of(k_bwd<T, W_, V_, N_, true>, kB);       \
+    static const KernelRes without = resources_of(k_bwd<T, W_, V_, N_, false>, kB);   \
+    *out = stats ? with : without;                                                    \
+    return hipSuccess;                                                                \
   }
   SY_TILES(X)
 #undef X
@@ -72,24 +143,21 @@ hipError_t SY_FN(launch_batched_vec_)(const sy_plan& p, const BatchedArgs& a, hi
 hipError_t SY_FN(launch_bwd_vec_)(const sy_plan& p, const BwdArgs& a, int grid, hipStream_t s) {
   const float inv_d = 1.0f / (float)a.d;
   const int64_t slots = (int64_t)grid * p.tokens_per_block;
-  const int n_iter = (int)((a.n_tok + slots - 1) / slots);
-#define X(W_, V_, N_)                                                                         \
-  if (tile_is(p, W_, V_, N_)) {                                                               \
-    hipLaunchKernelGGL((k_bwd<T, W_, V_, N_>), dim3(grid), dim3(BwdGeom<W_>::kBlock), 0, s,   \
-                       (const St*)a.v, (const St*)a.w, (const St*)a.g, a.stats, (St*)a.dv,     \
-                       a.partial, a.n_src, a.n_tok, a.d, a.src_stride, a.eps, inv_d, n_iter);  \
-    return hipGetLastError();                                                                 \
+  const int n_iter = (int)cdiv(a.n_tok, slots);
+#define X(W_, V_, N_)                                                                           \
+  if (tile_is(p, W_, V_, N_)) {                                                                 \
+    constexpr int kB = BwdGeom<W_>::kBlock;                                                     \
+    if (a.stats != nullptr) {                                                                   \
+      hipLaunchKernelGGL((k_bwd<T, W_, V_, N_, true>), dim3(grid), dim3(kB), 0, s,             \
+                         (const St*)a.v, (const St*)a.w, (const St*)a.g, a.stats, (St*)a.dv,     \
+                         a.partial, a.n_src, a.n_tok, a.d, a.src_stride, a.eps, inv_d, n_iter);  \
+    } else {                                                                                    \
+      hipLaunchKernelGGL((k_bwd<T, W_, V_, N_, false>), dim3(grid), dim3(kB), 0, s,            \
+                         (const St*)a.v, (const St*)a.w, (const St*)a.g, a.stats, (St*)a.dv,     \
+                         a.partial, a.n_src, a.n_tok, a.d, a.src_stride, a.eps, inv_d, n_iter);  \
+    }                                                                                           \
+    return hipGetLastError();                                                                   \
   }
-  SY_TILES(X)
-#undef X
-  return hipErrorInvalidConfiguration;
-}
-
-hipError_t SY_FN(bwd_vec_blocks_per_cu_)(const sy_plan& p, int* out) {
-#define X(W_, V_, N_)                                                                          \
-  if (tile_is(p, W_, V_, N_))                                                                  \
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(out, k_bwd<T, W_, V_, N_>,              \
-                                                        BwdGeom<W_>::kBlock, 0);
   SY_TILES(X)
 #undef X
   return hipErrorInvalidConfiguration;

@@ -120,7 +120,7 @@ k_fwd(const typename T::storage* __restrict__ v, const typename T::storage* __re
       if (n < rows) {
         const auto r = make_rsrc(v + (int64_t)(c0 + n) * src_stride + tok * d, row_bytes);
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) x[n][j] = ld16(r, lane_off + j * kStep);
+        for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
       }
     }
 
@@ -185,7 +185,7 @@ k_fwd(const typename T::storage* __restrict__ v, const typename T::storage* __re
     float f[CE];
 #pragma unroll
     for (int e = 0; e < CE; ++e) f[e] = acc[j][e] * inv_l;
-    st16(orr, lane_off + j * kStep, pack<T>(f));
+    st16_stream(orr, lane_off + j * kStep, pack<T>(f));
   }
 }
 
@@ -220,7 +220,7 @@ k_sol(const typename T::storage* __restrict__ v, typename T::storage* __restrict
       if (n < rows) {
         const auto r = make_rsrc(v + (int64_t)(c0 + n) * src_stride + tok * d, row_bytes);
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) x[n][j] = ld16(r, lane_off + j * kStep);
+        for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
       }
     }
 #pragma unroll
@@ -233,7 +233,7 @@ k_sol(const typename T::storage* __restrict__ v, typename T::storage* __restrict
   }
   const auto orr = make_rsrc(out + tok * d, row_bytes);
 #pragma unroll
-  for (int j = 0; j < VPL; ++j) st16(orr, lane_off + j * kStep, pack<T>(acc[j]));
+  for (int j = 0; j < VPL; ++j) st16_stream(orr, lane_off + j * kStep, pack<T>(acc[j]));
 }
 
 // ----------------------------------------------------------------- batched
@@ -272,7 +272,7 @@ k_batched(const typename T::storage* __restrict__ v, const typename T::storage* 
     if (n < rows) {
       const auto r = make_rsrc(v + (int64_t)n * src_stride + tok * d, row_bytes);
 #pragma unroll
-      for (int j = 0; j < VPL; ++j) x[n][j] = ld16(r, lane_off + j * kStep);
+      for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
     }
   }
   float rinv[NR];
@@ -339,17 +339,209 @@ k_batched(const typename T::storage* __restrict__ v, const typename T::storage* 
         float f[CE];
 #pragma unroll
         for (int e = 0; e < CE; ++e) f[e] = acc[j][e] * inv_l;
-        st16(orr, lane_off + j * kStep, pack<T>(f));
+        st16_stream(orr, lane_off + j * kStep, pack<T>(f));
       }
     }
   }
 }
 
+// ------------------------------------------- resident forward, pipelined
+//
+// Persistent variant of the forward for N <= NR (one chunk). Token slot s of
+// workgroup b handles tokens b*TPB + s + k*gridDim.x*TPB. The tile registers
+// are refilled as they are consumed: as soon as row n of the current token has
+// been accumulated into the output, row n of the slot's next token is loaded
+// into the same registers. The next token's loads are therefore in flight
+// during this token's weighted sum, output store and the loop overhead, with no
+// extra registers. `n_iter` is the slot trip count of the busiest slot; slots
+// with fewer tokens re-read their last token and store nothing, so when W > 1
+// every wave of the workgroup meets the same barriers.
+template <class T, int W, int VPL, int NR>
+__global__ void __launch_bounds__(FwdGeom<W>::kBlock)
+k_fwd_res(const typename T::storage* __restrict__ v, const typename T::storage* __restrict__ w,
+          typename T::storage* __restrict__ out, float* __restrict__ stats, int n_src,
+          int64_t n_tok, int d, int64_t src_stride, float eps, float inv_d, int n_iter) {
+  using S = typename T::storage;
+  constexpr int CE = T::ce;
+  constexpr int TPB = FwdGeom<W>::kTpb;
+  constexpr uint32_t kStep = 64u * W * 16u;
+  __shared__ float red[2][TPB][W][2 * NR];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int slot = wave / W;
+  const int seg = wave % W;
+  const int64_t slots = (int64_t)gridDim.x * TPB;
+  const int64_t first = (int64_t)blockIdx.x * TPB + slot;
+  int iters = n_iter;
+  if constexpr (W == 1) {
+    // Independent waves: each runs exactly its own tokens.
+    if (first >= n_tok) return;
+    iters = (int)((n_tok - first + slots - 1) / slots);
+  }
+  const uint32_t row_bytes = (uint32_t)d * sizeof(S);
+  const uint32_t lane_off = (uint32_t)(seg * 64 + lane) * 16u;
+  const int rows = n_src;  // host guarantees n_src <= NR
+
+  i32x4_t wq[VPL];
+  {
+    const auto wr = make_rsrc(w, row_bytes);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) wq[j] = ld16(wr, lane_off + j * kStep);
+  }
+  i32x4_t x[NR][VPL];
+  {
+    const int64_t t0 = first < n_tok ? first : n_tok - 1;
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      if (n < rows) {
+        const auto r = make_rsrc(v + (int64_t)n * src_stride + t0 * d, row_bytes);
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
+      }
+    }
+  }
+
+  for (int k = 0; k < iters; ++k) {
+    const int64_t tok = first + (int64_t)k * slots;
+    const bool live = tok < n_tok;
+    const bool more = k + 1 < iters;
+    const int64_t nxt = tok + slots < n_tok ? tok + slots : n_tok - 1;
+
+    float part[2 * NR];
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      if (n < rows) {
+        float ss = 0.0f, dt = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+          ss = dot<T>(x[n][j], x[n][j], ss);
+          dt = dot<T>(x[n][j], wq[j], dt);
+        }
+        part[n] = wave_sum(ss);
+        part[NR + n] = wave_sum(dt);
+      }
+    }
+    if constexpr (W > 1) cross_wave_sum<W, 2, NR, TPB>(part, 2, rows, red[k & 1], slot, seg, lane);
+
+    float lg[NR];
+    float m = -INFINITY;
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      if (n < rows) {
+        const float r = rsqrtf(fmaf(part[n], inv_d, eps));
+        lg[n] = part[NR + n] * r;
+        part[n] = r;
+        m = fmaxf(m, lg[n]);
+      }
+    }
+    float acc[VPL][CE];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+#pragma unroll
+      for (int e = 0; e < CE; ++e) acc[j][e] = 0.0f;
+    float l = 0.0f;
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      if (n < rows) {
+        const float p = expf(lg[n] - m);
+        l += p;
+#pragma unroll
+        for (int j = 0; j < VPL; ++j)
+#pragma unroll
+          for (int e = 0; e < CE; ++e) acc[j][e] = fmaf(p, elem<T>(x[n][j], e), acc[j][e]);
+        if (more) {
+          const auto r = make_rsrc(v + (int64_t)n * src_stride + nxt * d, row_bytes);
+#pragma unroll
+          for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
+        }
+      }
+    }
+    if (live) {
+      if (stats != nullptr && seg == 0 && lane == 0) {
+#pragma unroll
+        for (int n = 0; n < NR; ++n) {
+          if (n < rows) {
+            stats[(int64_t)n * n_tok + tok] = lg[n];
+            stats[(int64_t)(n_src + n) * n_tok + tok] = part[n];
+          }
+        }
+      }
+      const float inv_l = 1.0f / l;
+      const auto orr = make_rsrc(out + tok * d, row_bytes);
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) {
+        float f[CE];
+#pragma unroll
+        for (int e = 0; e < CE; ++e) f[e] = acc[j][e] * inv_l;
+        st16_stream(orr, lane_off + j * kStep, pack<T>(f));
+      }
+    }
+  }
+}
+
+// ------------------------------------------ resident speed of light, pipelined
+//
+// The ceiling for k_fwd_res: same bytes, grid, slot loop and prefetch, no
+// softmax (out = sum_n v_n).
+template <class T, int W, int VPL, int NR>
+__global__ void __launch_bounds__(FwdGeom<W>::kBlock)
+k_sol_res(const typename T::storage* __restrict__ v, typename T::storage* __restrict__ out,
+          int n_src, int64_t n_tok, int d, int64_t src_stride) {
+  using S = typename T::storage;
+  constexpr int CE = T::ce;
+  constexpr int TPB = FwdGeom<W>::kTpb;
+  constexpr uint32_t kStep = 64u * W * 16u;
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int64_t slots = (int64_t)gridDim.x * TPB;
+  const int64_t first = (int64_t)blockIdx.x * TPB + wave / W;
+  if (first >= n_tok) return;  // no barriers in this kernel
+  const int iters = (int)((n_tok - first + slots - 1) / slots);
+  const uint32_t row_bytes = (uint32_t)d * sizeof(S);
+  const uint32_t lane_off = (uint32_t)((wave % W) * 64 + lane) * 16u;
+  const int rows = n_src;
+
+  i32x4_t x[NR][VPL];
+#pragma unroll
+  for (int n = 0; n < NR; ++n) {
+    if (n < rows) {
+      const auto r = make_rsrc(v + (int64_t)n * src_stride + first * d, row_bytes);
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
+    }
+  }
+  for (int k = 0; k < iters; ++k) {
+    const int64_t tok = first + (int64_t)k * slots;
+    const bool more = k + 1 < iters;
+    float acc[VPL][CE];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+#pragma unroll
+      for (int e = 0; e < CE; ++e) acc[j][e] = 0.0f;
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      if (n < rows) {
+#pragma unroll
+        for (int j = 0; j < VPL; ++j)
+#pragma unroll
+          for (int e = 0; e < CE; ++e) acc[j][e] += elem<T>(x[n][j], e);
+        if (more) {
+          const auto r = make_rsrc(v + (int64_t)n * src_stride + (tok + slots) * d, row_bytes);
+#pragma unroll
+          for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
+        }
+      }
+    }
+    const auto orr = make_rsrc(out + tok * d, row_bytes);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) st16_stream(orr, lane_off + j * kStep, pack<T>(acc[j]));
+  }
+}
+
 // ----------------------------------------------------------------- backward
 //
-// Persistent: workgroup b owns token slots b*TPB + slot + k*gridDim.x*TPB for
-// k < n_iter (the same trip count for every slot, so barriers line up; slots
-// past the end re-read the last token and store nothing). Per token, with
+// Persistent and pipelined like k_fwd_res (N <= NR). Per token, with
 // r_n = rsqrt(ssq_n/D + eps), logit_n = a_n r_n, alpha = softmax(logit),
 // G_n = <g, v_n> (derivation of triton_op.py:205-214):
 //     S        = sum_n alpha_n G_n
@@ -358,11 +550,14 @@ k_batched(const typename T::storage* __restrict__ v, const typename T::storage* 
 //     c_n      = 2 dssq_n = -dlogit_n a_n r_n^3 / D = -dlogit_n logit_n r_n^2 / D
 //     dv_n     = alpha_n g + da_n w + c_n v_n
 //     dw      += sum_n da_n v_n
-// With stats (logit_n, r_n from the forward) only G_n is reduced over D.
+// STATS: logit_n and r_n come from the forward's stats, so only G_n is reduced
+// over D; otherwise a_n and ssq_n are recomputed as in the forward.
+// grad_out and each source row are refilled with the next token's data as soon
+// as they have been consumed.
 // dw: each slot accumulates in registers; at the end the slots are folded in
 // a fixed tree through LDS and the workgroup writes one fp32 row of `partial`.
 // No float atomics anywhere, so dw is bit-reproducible for a given grid.
-template <class T, int W, int VPL, int NR>
+template <class T, int W, int VPL, int NR, bool STATS>
 __global__ void __launch_bounds__(BwdGeom<W>::kBlock)
 k_bwd(const typename T::storage* __restrict__ v, const typename T::storage* __restrict__ w,
       const typename T::storage* __restrict__ g, const float* __restrict__ stats,
@@ -373,12 +568,13 @@ k_bwd(const typename T::storage* __restrict__ v, const typename T::storage* __re
   constexpr int TPB = BwdGeom<W>::kTpb;
   constexpr uint32_t kStep = 64u * W * 16u;
   constexpr int kLaneFloats = VPL * CE;  // dw values a lane accumulates
+  constexpr int G = STATS ? 1 : 3;       // per-row scalars reduced over D
   // Slot fold buffer: the upper half of the live slots parks its dw here. The
   // +1 pad keeps the lane-strided writes free of bank conflicts.
   constexpr int kFH = TPB > 1 ? TPB / 2 : 1;
   constexpr int kFW = TPB > 1 ? W : 1;
   constexpr int kFL = TPB > 1 ? 64 : 1;
-  __shared__ float red[2][TPB][W][3 * NR];
+  __shared__ float red[2][TPB][W][G * NR];
   __shared__ float fold[kFH][kFW][kFL][kLaneFloats + 1];
 
   const int lane = threadIdx.x & 63;
@@ -388,14 +584,25 @@ k_bwd(const typename T::storage* __restrict__ v, const typename T::storage* __re
   const uint32_t row_bytes = (uint32_t)d * sizeof(S);
   const uint32_t lane_off = (uint32_t)(seg * 64 + lane) * 16u;
   const int64_t slots = (int64_t)gridDim.x * TPB;
+  const int64_t first = (int64_t)blockIdx.x * TPB + slot;
   const int64_t dv_stride = n_tok * d;
   const int rows = n_src;  // host guarantees n_src <= NR
+  int iters = n_iter;
+  if constexpr (W == 1) {
+    // No barrier inside the loop: each wave runs only its own tokens.
+    iters = first < n_tok ? (int)((n_tok - first + slots - 1) / slots) : 0;
+  }
 
+  float wf[VPL][CE];
   i32x4_t wq[VPL];
   {
     const auto wr = make_rsrc(w, row_bytes);
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) wq[j] = ld16(wr, lane_off + j * kStep);
+    for (int j = 0; j < VPL; ++j) {
+      wq[j] = ld16(wr, lane_off + j * kStep);
+#pragma unroll
+      for (int e = 0; e < CE; ++e) wf[j][e] = elem<T>(wq[j], e);
+    }
   }
   float dwa[VPL][CE];
 #pragma unroll
@@ -403,31 +610,33 @@ k_bwd(const typename T::storage* __restrict__ v, const typename T::storage* __re
 #pragma unroll
     for (int e = 0; e < CE; ++e) dwa[j][e] = 0.0f;
 
-  for (int k = 0; k < n_iter; ++k) {
-    int64_t tok = (int64_t)blockIdx.x * TPB + slot + k * slots;
-    const bool live = tok < n_tok;
-    if (!live) tok = n_tok - 1;
-
-    i32x4_t x[NR][VPL];
+  i32x4_t x[NR][VPL];
+  i32x4_t gq[VPL];
+  {
+    const int64_t t0 = first < n_tok ? first : n_tok - 1;
 #pragma unroll
     for (int n = 0; n < NR; ++n) {
       if (n < rows) {
-        const auto r = make_rsrc(v + (int64_t)n * src_stride + tok * d, row_bytes);
+        const auto r = make_rsrc(v + (int64_t)n * src_stride + t0 * d, row_bytes);
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) x[n][j] = ld16(r, lane_off + j * kStep);
+        for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
       }
     }
-    i32x4_t gq[VPL];
-    {
-      const auto gr = make_rsrc(g + tok * d, row_bytes);
+    const auto gr = make_rsrc(g + t0 * d, row_bytes);
 #pragma unroll
-      for (int j = 0; j < VPL; ++j) gq[j] = ld16(gr, lane_off + j * kStep);
-    }
+    for (int j = 0; j < VPL; ++j) gq[j] = ld16_stream(gr, lane_off + j * kStep);
+  }
 
-    // Per-row scalars: part[n] grad dot, then (without stats) part[NR + n]
-    // query dot and part[2*NR + n] sum of squares.
-    const bool have_stats = stats != nullptr;
-    float part[3 * NR];
+  for (int k = 0; k < iters; ++k) {
+    const int64_t tok_raw = first + (int64_t)k * slots;
+    const bool live = tok_raw < n_tok;
+    const int64_t tok = live ? tok_raw : n_tok - 1;
+    const bool more = k + 1 < iters;
+    const int64_t nxt = tok_raw + slots < n_tok ? tok_raw + slots : n_tok - 1;
+
+    // part[n] grad dot; without stats also part[NR + n] query dot and
+    // part[2*NR + n] sum of squares.
+    float part[G * NR];
 #pragma unroll
     for (int n = 0; n < NR; ++n) {
       if (n < rows) {
@@ -435,7 +644,7 @@ k_bwd(const typename T::storage* __restrict__ v, const typename T::storage* __re
 #pragma unroll
         for (int j = 0; j < VPL; ++j) gg = dot<T>(x[n][j], gq[j], gg);
         part[n] = wave_sum(gg);
-        if (!have_stats) {
+        if constexpr (!STATS) {
           float dt = 0.0f, ss = 0.0f;
 #pragma unroll
           for (int j = 0; j < VPL; ++j) {
@@ -447,15 +656,14 @@ k_bwd(const typename T::storage* __restrict__ v, const typename T::storage* __re
         }
       }
     }
-    if constexpr (W > 1)
-      cross_wave_sum<W, 3, NR, TPB>(part, have_stats ? 1 : 3, rows, red[k & 1], slot, seg, lane);
+    if constexpr (W > 1) cross_wave_sum<W, G, NR, TPB>(part, G, rows, red[k & 1], slot, seg, lane);
 
     float lg[NR], rr[NR];
     float m = -INFINITY;
 #pragma unroll
     for (int n = 0; n < NR; ++n) {
       if (n < rows) {
-        if (have_stats) {
+        if constexpr (STATS) {
           lg[n] = stats[(int64_t)n * n_tok + tok];
           rr[n] = stats[(int64_t)(n_src + n) * n_tok + tok];
         } else {
@@ -482,14 +690,16 @@ k_bwd(const typename T::storage* __restrict__ v, const typename T::storage* __re
         sdot = fmaf(al[n], part[n], sdot);
       }
 
-    float gf[VPL][CE], wf[VPL][CE];
+    float gf[VPL][CE];
 #pragma unroll
     for (int j = 0; j < VPL; ++j)
 #pragma unroll
-      for (int e = 0; e < CE; ++e) {
-        gf[j][e] = elem<T>(gq[j], e);
-        wf[j][e] = elem<T>(wq[j], e);
-      }
+      for (int e = 0; e < CE; ++e) gf[j][e] = elem<T>(gq[j], e);
+    if (more) {
+      const auto gr = make_rsrc(g + nxt * d, row_bytes);
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) gq[j] = ld16_stream(gr, lane_off + j * kStep);
+    }
     const float dw_on = live ? 1.0f : 0.0f;
 #pragma unroll
     for (int n = 0; n < NR; ++n) {
@@ -508,7 +718,12 @@ k_bwd(const typename T::storage* __restrict__ v, const typename T::storage* __re
             f[e] = fmaf(c, xv, fmaf(da, wf[j][e], al[n] * gf[j][e]));
             dwa[j][e] = fmaf(da_w, xv, dwa[j][e]);
           }
-          st16(dr, lane_off + j * kStep, pack<T>(f));
+          st16_stream(dr, lane_off + j * kStep, pack<T>(f));
+        }
+        if (more) {
+          const auto r = make_rsrc(v + (int64_t)n * src_stride + nxt * d, row_bytes);
+#pragma unroll
+          for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
         }
       }
     }

@@ -78,14 +78,25 @@ void apply_tile_override(int op, int64_t n_src, int64_t d, sy_plan* p);
 // Device queries, cached per device (sy_capi.cpp).
 hipError_t cu_count(int* out);
 
+// Register/LDS footprint of one kernel instantiation, the workgroups per CU
+// that footprint allows, and (when filled by a launcher) the launch grid.
+struct KernelRes {
+  int vgprs;
+  int lds;
+  int blocks_per_cu;
+  int grid;
+};
+
 // Per-dtype vector-kernel launchers (sy_inst.hip built once per dtype).
+// launch_fwd_vec_* with `info` != nullptr fills it and launches nothing.
 // `grid` for the backward is the persistent workgroup count.
 #define SY_DECLARE_VEC(NAME)                                                                   \
-  hipError_t launch_fwd_vec_##NAME(const sy_plan& p, const FwdArgs& a, hipStream_t s);         \
+  hipError_t launch_fwd_vec_##NAME(const sy_plan& p, const FwdArgs& a, hipStream_t s,          \
+                                   KernelRes* info);                                           \
   hipError_t launch_sol_vec_##NAME(const sy_plan& p, const FwdArgs& a, hipStream_t s);         \
   hipError_t launch_batched_vec_##NAME(const sy_plan& p, const BatchedArgs& a, hipStream_t s); \
   hipError_t launch_bwd_vec_##NAME(const sy_plan& p, const BwdArgs& a, int grid, hipStream_t s); \
-  hipError_t bwd_vec_blocks_per_cu_##NAME(const sy_plan& p, int* out);
+  hipError_t bwd_vec_resources_##NAME(const sy_plan& p, bool stats, KernelRes* out);
 SY_DECLARE_VEC(bf16)
 SY_DECLARE_VEC(f16)
 SY_DECLARE_VEC(f32)

@@ -5,9 +5,10 @@
 // Rules, in order:
 //  1. Vector kernels need every row start 16-byte aligned, D a multiple of the
 //     chunk width, and (forward/backward) w in v's dtype. Otherwise: generic.
-//  2. Prefer the fewest waves per token whose chunks-per-lane is 1, 2 or 4 and
-//     whose resident tile (rows_per_tile x chunks_per_lane 16-byte chunks,
-//     four VGPRs each) fits the op's budget with rows_per_tile >= N.
+//  2. Prefer the fewest waves per token whose chunks-per-lane is 1, 2 or 4
+//     (backward: 1 or 2) and whose resident tile (rows_per_tile x
+//     chunks_per_lane 16-byte chunks, four VGPRs each) fits the op's budget
+//     with rows_per_tile >= N.
 //  3. Forward / speed-of-light with no resident fit: online-softmax chunks of
 //     the largest tile that fits.
 //  4. Backward with no resident fit under its budget: generic (a fatter tile
@@ -61,11 +62,13 @@ void set(sy_plan* p, int family, int w, int vpl, int nr, int ce, int op, int64_t
   p->n_chunks = (int)((n_src + nr - 1) / nr);
 }
 
-// Resident plan with rows_per_tile >= n_src under `budget`; false if none.
-bool resident(int64_t n_src, int64_t e, int budget, int* w_out, int* vpl_out, int* nr_out) {
+// Resident plan with rows_per_tile >= n_src under `budget` and at most
+// `max_vpl` chunks per lane; false if none.
+bool resident(int64_t n_src, int64_t e, int budget, int max_vpl, int* w_out, int* vpl_out,
+              int* nr_out) {
   for (int w : kWaves) {
     const int vpl = round_vpl((e + 64 * w - 1) / (64 * w));
-    if (vpl == 0) continue;
+    if (vpl == 0 || vpl > max_vpl) continue;
     for (int nr : kRows) {
       if (!tile_exists(vpl, nr) || nr < n_src || nr * vpl > budget) continue;
       *w_out = w;
@@ -96,7 +99,10 @@ int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_
   if (vec && !(op == SY_OP_BATCHED && n_q > kBatchedMaxQ)) {
     const int budget =
         op == SY_OP_BWD ? kBwdBudget : (op == SY_OP_BATCHED ? kBatchedBudget : kFwdBudget);
-    if (resident(n_src, e, budget, &w, &vpl, &nr)) {
+    // The backward keeps grad_out, w (raw and fp32) and dw accumulators next
+    // to the tile: with 4 chunks per lane some of its variants spill.
+    const int max_vpl = op == SY_OP_BWD ? 2 : 4;
+    if (resident(n_src, e, budget, max_vpl, &w, &vpl, &nr)) {
       set(out, SY_FAMILY_RESIDENT, w, vpl, nr, ce, op, n_src);
       return SY_OK;
     }

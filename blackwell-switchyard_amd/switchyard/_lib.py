@@ -56,6 +56,11 @@ SIGNATURES = {
     "sy_bwd_workspace_bytes": (_i64, [_i64, _i64, _i64, _i32, _i32]),
     "sy_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32, _i32,
                       ctypes.c_float, _vp]),
+    "sy_bwd_partial_rows": (_i64, [_i64, _i64, _i64, _i32, _i32, _i32, _i32]),
+    "sy_kernel_info": (_i32, [_i32, _i64, _i64, _i64, _i32, _i32, ctypes.POINTER(ctypes.c_int32)]),
+    "sy_bwd_main": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32, _i32,
+                           ctypes.c_float, _vp]),
+    "sy_dw_reduce": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp]),
     "sy_fwd_batched": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32, ctypes.c_float, _vp]),
     "sy_sol": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp]),
     "sy_bw_probe": (_i32, [_i32, _vp, _vp, _i64, _vp]),

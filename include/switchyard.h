@@ -110,6 +110,22 @@ int sy_bwd(const void* v, const void* w, const void* grad_out, const float* stat
            void* dw, void* workspace, int64_t workspace_bytes, int64_t n_src, int64_t n_tok,
            int64_t d, int64_t src_stride, int v_dtype, int w_dtype, float eps, void* stream);
 
+/* The two stages of sy_bwd, separately launchable (to time them, or to run the
+ * small dw reduction later on another stream). sy_bwd == sy_bwd_main followed
+ * by sy_dw_reduce over sy_bwd_partial_rows() rows of the workspace.
+ * sy_bwd_partial_rows returns the row count (0 when n_tok == 0) or < 0 on bad
+ * input; `aligned` as in sy_plan_for, `has_stats` whether stats will be
+ * passed. sy_bwd_main writes dv and the fp32 partials [rows][D];
+ * sy_dw_reduce writes dw[c] = sum_r partial[r][c] in a fixed order, cast to
+ * w_dtype. Same reference interface as sy_bwd. */
+int64_t sy_bwd_partial_rows(int64_t n_src, int64_t n_tok, int64_t d, int v_dtype, int w_dtype,
+                            int aligned, int has_stats);
+int sy_bwd_main(const void* v, const void* w, const void* grad_out, const float* stats, void* dv,
+                void* workspace, int64_t workspace_bytes, int64_t n_src, int64_t n_tok, int64_t d,
+                int64_t src_stride, int v_dtype, int w_dtype, float eps, void* stream);
+int sy_dw_reduce(const float* partial, int64_t rows, int64_t d, void* dw, int w_dtype,
+                 void* stream);
+
 /* Output-only batched forward: out[s] = AttnRes(v, queries[s]) for S queries
  * sharing one read of v. queries has v's dtype.
  * Replaces block_attn_res_batched/_fwd_batched_resident
@@ -129,6 +145,13 @@ int sy_sol(const void* v, void* out, int64_t n_src, int64_t n_tok, int64_t d,
  * bench/machine.py:41-61. */
 int sy_bw_probe(int kind, const void* src, void* dst, int64_t bytes, void* stream);
 int64_t sy_probe_grid(int64_t bytes);
+
+/* Resources of the kernel a plan selects on the current device:
+ * out[0] VGPRs per lane, out[1] static LDS bytes per workgroup, out[2] the
+ * workgroups per CU the library assumes, out[3] the launch grid for n_tok
+ * tokens. Diagnostics only; no reference counterpart. */
+int sy_kernel_info(int op, int64_t n_src, int64_t n_tok, int64_t d, int v_dtype, int w_dtype,
+                   int32_t out[4]);
 
 /* Static string for a status code (negative sy_status or positive hipError_t). */
 const char* sy_strerror(int code);
