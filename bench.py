@@ -25,6 +25,9 @@ Modes:
   python bench.py --kernel {fwd,bwd,reduce,sol,copy} --iters K
                                                 run one kernel K times (for rocprofv3)
   python bench.py --summarize DIR --title T     rocprofv3 CSV -> markdown summary
+  python bench.py --traffic FETCH_DIR WRITE_DIR --json-out F
+                                                rocprofv3 --pmc runs of --kernel all ->
+                                                calibrated HBM bytes per launch (JSON)
 """
 
 from __future__ import annotations
@@ -68,11 +71,12 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--cpu-budget-s", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip flushed latency, kernel count, memory")
-    ap.add_argument("--kernel", choices=["fwd", "bwd", "reduce", "sol", "copy"], default=None)
+    ap.add_argument("--kernel", choices=["fwd", "bwd", "reduce", "sol", "copy", "all"], default=None)
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--summarize", type=pathlib.Path, default=None)
     ap.add_argument("--title", default="")
     ap.add_argument("--json-out", type=pathlib.Path, default=None)
+    ap.add_argument("--traffic", nargs=2, type=pathlib.Path, default=None, metavar=("FETCH_DIR", "WRITE_DIR"))
     return ap.parse_args()
 
 
@@ -273,7 +277,8 @@ def cpu_baseline_leg(wl, args, torch):
 
 
 def run_kernel_mode(args):
-    """Launch one kernel --iters times over the rotating sets (rocprofv3 target)."""
+    """Launch kernels --iters times over the rotating sets (rocprofv3 target).
+    ``all`` runs fwd, bwd, reduce, sol and the 1 GiB copy probe in turn."""
     import torch
 
     from switchyard import harness
@@ -281,25 +286,26 @@ def run_kernel_mode(args):
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    if args.kernel == "copy":
-        nbytes = 1 << 30
-        src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(3)
-        dst = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-        for _ in range(args.iters):
-            bandwidth_probe("copy", src, dst)
-        torch.cuda.synchronize(dev)
-        log(f"copy probe: {args.iters} x {nbytes} bytes")
-        return
-    wl = Workload(args, torch, dev)
-    for s in wl.sets:  # stats/partials must exist for bwd/reduce
-        wl.fwd(s)
-        if args.kernel == "reduce":
+    kinds = ["fwd", "bwd", "reduce", "sol", "copy"] if args.kernel == "all" else [args.kernel]
+    wl = None
+    if any(k != "copy" for k in kinds):
+        wl = Workload(args, torch, dev)
+        for s in wl.sets:  # stats and partials must exist for bwd / reduce
+            wl.fwd(s)
             wl.bwd_main(s)
-    torch.cuda.synchronize(dev)
-    name = {"fwd": "fwd", "bwd": "bwd_main", "reduce": "reduce", "sol": "sol"}[args.kernel]
-    fns = wl.closures(name)
-    ms = harness.time_loop(fns, device=dev, iters=args.iters)
-    log(f"{args.kernel}: {args.iters} launches, {ms * 1e3:.2f} us average (HIP events)")
+        torch.cuda.synchronize(dev)
+    for kind in kinds:
+        if kind == "copy":
+            nbytes = 1 << 30
+            src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(3)
+            dst = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+            ms = harness.time_loop([lambda: bandwidth_probe("copy", src, dst)], device=dev, iters=args.iters)
+            log(f"copy: {args.iters} x {nbytes} bytes, {ms * 1e3:.2f} us average")
+            del src, dst
+            continue
+        name = {"fwd": "fwd", "bwd": "bwd_main", "reduce": "reduce", "sol": "sol"}[kind]
+        ms = harness.time_loop(wl.closures(name), device=dev, iters=args.iters)
+        log(f"{kind}: {args.iters} launches, {ms * 1e3:.2f} us average (HIP events)")
 
 
 def summarize(args):
@@ -331,8 +337,58 @@ def summarize(args):
     print("\n".join(lines))
 
 
+def _counter_means(d: pathlib.Path, counter: str) -> dict[str, float]:
+    import csv
+
+    agg: dict[str, list[float]] = {}
+    for f in sorted(d.rglob("*counter_collection.csv")):
+        with open(f) as fh:
+            for row in csv.DictReader(fh):
+                if row.get("Counter_Name") == counter:
+                    agg.setdefault(row.get("Kernel_Name") or "?", []).append(float(row.get("Counter_Value") or 0))
+    return {k: sum(v) / len(v) for k, v in agg.items()}
+
+
+def traffic_mode(args):
+    """HBM bytes per launch from FETCH_SIZE / WRITE_SIZE (KiB per dispatch),
+    each scaled so the 1 GiB copy probe reads and writes exactly 1 GiB."""
+    fetch = _counter_means(args.traffic[0], "FETCH_SIZE")
+    write = _counter_means(args.traffic[1], "WRITE_SIZE")
+
+    def pick(table, needle):
+        hits = [v for k, v in table.items() if needle in k]
+        if not hits:
+            raise SystemExit(f"no dispatch of {needle} in the counter data")
+        return hits[0]
+
+    gib_kib = float(1 << 20)
+    fscale = gib_kib / pick(fetch, "k_probe_copy")
+    wscale = gib_kib / pick(write, "k_probe_copy")
+    slab = args.b * args.t * args.d * 2
+    algo = {"k_fwd_res": (args.n + 1) * slab, "k_bwd<": (2 * args.n + 1) * slab, "k_sol_res": (args.n + 1) * slab}
+    rec = {"workload": f"N={args.n} B={args.b} T={args.t} D={args.d} bf16", "fetch_scale": fscale,
+           "write_scale": wscale, "method": "rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE (KiB per dispatch), "
+           "each scaled by what the counter reads for the 1 GiB copy probe"}
+    for needle, nbytes in algo.items():
+        f_kib, w_kib = pick(fetch, needle), pick(write, needle)
+        tot = (f_kib * fscale + w_kib * wscale) * 1024
+        key = {"k_fwd_res": "fwd", "k_bwd<": "bwd_main", "k_sol_res": "sol"}[needle]
+        rec[f"{key}_bytes_per_launch"] = round(tot)
+        rec[f"{key}_fetch_kib"] = f_kib
+        rec[f"{key}_write_kib"] = w_kib
+        rec[f"{key}_algorithmic_bytes"] = nbytes
+        rec[f"{key}_traffic_over_algorithmic"] = tot / nbytes
+    line = json.dumps(rec, indent=1)
+    if args.json_out:
+        args.json_out.write_text(line + "\n")
+    print(line)
+
+
 def main() -> None:
     args = parse_args()
+    if args.traffic is not None:
+        traffic_mode(args)
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus > 1 or world > 1:
         print("bench.py: this build measures one GPU only (the operator is independent per token; "

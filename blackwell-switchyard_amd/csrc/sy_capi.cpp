@@ -326,9 +326,11 @@ int sy_fwd_batched(const void* v, const void* queries, void* out, int64_t n_src,
 }
 
 int64_t sy_probe_grid(int64_t bytes) {
+  // 256 threads x 4 chunks in flight per workgroup; up to 32768 workgroups
+  // (the grid that reached the highest read bandwidth on MI355X).
   if (bytes <= 0) return 1;
-  const int64_t g = (bytes / 16 + 255) / 256;
-  return g < 1 ? 1 : (g > 4096 ? 4096 : g);
+  const int64_t g = (bytes / 16 + 1023) / 1024;
+  return g < 1 ? 1 : (g > 32768 ? 32768 : g);
 }
 
 int sy_bw_probe(int kind, const void* src, void* dst, int64_t bytes, void* stream) {

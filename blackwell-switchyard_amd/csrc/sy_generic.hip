@@ -185,20 +185,27 @@ k_bwd_generic(const void* __restrict__ v, const void* __restrict__ w, const void
       m = fmaxf(m, al[n]);
     }
     m = block_max(m, scr);
+    // gref = grad dot of the first row with the largest logit: the softmax
+    // backward is evaluated relative to it (see k_bwd) to avoid cancellation.
+    float first = (float)n_src;
+    for (int n = tid; n < n_src; n += kBlock)
+      if (al[n] == m) first = fminf(first, (float)n);
+    first = -block_max(-first, scr);
+    const float gref = gc[min((int)first, n_src - 1)];
     float l = 0.0f, sp = 0.0f;
     for (int n = tid; n < n_src; n += kBlock) {
       const float p = expf(al[n] - m);
       l += p;
-      sp = fmaf(p, gc[n], sp);
+      sp = fmaf(p, gc[n] - gref, sp);
     }
     l = block_sum(l, scr);
     sp = block_sum(sp, scr);
     const float inv_l = 1.0f / l;
-    const float sdot = sp * inv_l;
+    const float sdev = sp * inv_l;
     for (int n = tid; n < n_src; n += kBlock) {
       const float lgn = al[n], r = da[n];
       const float a = expf(lgn - m) * inv_l;
-      const float dlogit = a * (gc[n] - sdot);
+      const float dlogit = a * ((gc[n] - gref) - sdev);
       al[n] = a;
       da[n] = dlogit * r;
       gc[n] = -dlogit * lgn * r * r * inv_d;

@@ -545,7 +545,7 @@ k_sol_res(const typename T::storage* __restrict__ v, typename T::storage* __rest
 // r_n = rsqrt(ssq_n/D + eps), logit_n = a_n r_n, alpha = softmax(logit),
 // G_n = <g, v_n> (derivation of triton_op.py:205-214):
 //     S        = sum_n alpha_n G_n
-//     dlogit_n = alpha_n (G_n - S)
+//     dlogit_n = alpha_n (G_n - S)      [evaluated relative to the top row's G]
 //     da_n     = dlogit_n r_n
 //     c_n      = 2 dssq_n = -dlogit_n a_n r_n^3 / D = -dlogit_n logit_n r_n^2 / D
 //     dv_n     = alpha_n g + da_n w + c_n v_n
@@ -658,8 +658,13 @@ k_bwd(const typename T::storage* __restrict__ v, const typename T::storage* __re
     }
     if constexpr (W > 1) cross_wave_sum<W, G, NR, TPB>(part, G, rows, red[k & 1], slot, seg, lane);
 
+    // gref = G of the row with the largest logit. Measuring G from it makes
+    // the softmax backward free of cancellation: G_n - S equals
+    // (G_n - gref) - sum_k alpha_k (G_k - gref), in which the dominant row's
+    // term is exactly zero, so a saturated softmax (alpha_max -> 1) still gets
+    // its tiny dlogit to full relative precision instead of G_max - S ~ 0.
     float lg[NR], rr[NR];
-    float m = -INFINITY;
+    float m = -INFINITY, gref = 0.0f;
 #pragma unroll
     for (int n = 0; n < NR; ++n) {
       if (n < rows) {
@@ -670,7 +675,10 @@ k_bwd(const typename T::storage* __restrict__ v, const typename T::storage* __re
           rr[n] = rsqrtf(fmaf(part[2 * NR + n], inv_d, eps));
           lg[n] = part[NR + n] * rr[n];
         }
-        m = fmaxf(m, lg[n]);
+        if (lg[n] > m) {
+          m = lg[n];
+          gref = part[n];
+        }
       }
     }
     float al[NR];
@@ -682,12 +690,13 @@ k_bwd(const typename T::storage* __restrict__ v, const typename T::storage* __re
         l += al[n];
       }
     const float inv_l = 1.0f / l;
-    float sdot = 0.0f;
+    float sdev = 0.0f;
 #pragma unroll
     for (int n = 0; n < NR; ++n)
       if (n < rows) {
         al[n] *= inv_l;
-        sdot = fmaf(al[n], part[n], sdot);
+        part[n] -= gref;
+        sdev = fmaf(al[n], part[n], sdev);
       }
 
     float gf[VPL][CE];
@@ -704,7 +713,7 @@ k_bwd(const typename T::storage* __restrict__ v, const typename T::storage* __re
 #pragma unroll
     for (int n = 0; n < NR; ++n) {
       if (n < rows) {
-        const float dlogit = al[n] * (part[n] - sdot);
+        const float dlogit = al[n] * (part[n] - sdev);
         const float da = dlogit * rr[n];
         const float c = -dlogit * lg[n] * rr[n] * rr[n] * inv_d;
         const float da_w = da * dw_on;

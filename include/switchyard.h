@@ -140,7 +140,8 @@ int sy_sol(const void* v, void* out, int64_t n_src, int64_t n_tok, int64_t d,
            int64_t src_stride, int dtype, void* stream);
 
 /* HBM probes over `bytes` (a multiple of 16): kind 0 = read src (dst receives
- * one float per workgroup, dst must hold sy_probe_grid(bytes) floats),
+ * one float per workgroup, dst must hold sy_probe_grid(bytes) floats, at most
+ * 32768),
  * 1 = write dst, 2 = copy src -> dst. Replaces the copy/read/write probes of
  * bench/machine.py:41-61. */
 int sy_bw_probe(int kind, const void* src, void* dst, int64_t bytes, void* stream);

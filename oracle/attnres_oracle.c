@@ -75,6 +75,9 @@ int oracle_forward(const double* v, const double* w, double* out, double* alpha_
  *   dlogit_n = alpha_n (G_n - S), da_n = dlogit_n r_n,
  *   dssq_n = -dlogit_n a_n r_n^3 / (2D),
  *   dv_n = alpha_n g + da_n w + 2 dssq_n v_n,  dw = sum_tokens sum_n da_n v_n.
+ * G_n - S is evaluated as (G_n - G_m) - sum_k alpha_k (G_k - G_m), m the
+ * row with the largest logit: the same number (alpha sums to one), but with
+ * no cancellation when the softmax saturates (alpha_m -> 1, G_m - S -> 0).
  * dv [N][T][D], dw [D] (overwritten). */
 int oracle_backward(const double* v, const double* w, const double* g, double* dv, double* dw,
                     int64_t n, int64_t t, int64_t d, double eps) {
@@ -86,20 +89,23 @@ int oracle_backward(const double* v, const double* w, const double* g, double* d
   for (int64_t tok = 0; tok < t; ++tok) {
     token_alpha(v, w, n, t, tok, d, eps, logit, alpha, rinv);
     const double* gt = g + tok * d;
-    double s = 0.0;
+    int64_t top = 0;
     for (int64_t i = 0; i < n; ++i) {
       const double* x = v + (i * t + tok) * d;
       double gg = 0.0;
       for (int64_t k = 0; k < d; ++k) gg += gt[k] * x[k];
       gdot[i] = gg;
-      s += alpha[i] * gg;
+      if (logit[i] > logit[top]) top = i;
     }
+    const double gref = gdot[top];
+    double s = 0.0; /* S - G_top */
+    for (int64_t i = 0; i < n; ++i) s += alpha[i] * (gdot[i] - gref);
     for (int64_t i = 0; i < n; ++i) {
       const double* x = v + (i * t + tok) * d;
       double* dx = dv + (i * t + tok) * d;
       const double r = rinv[i];
       const double a = logit[i] / r; /* <w, v_i> */
-      const double dlogit = alpha[i] * (gdot[i] - s);
+      const double dlogit = alpha[i] * ((gdot[i] - gref) - s);
       const double da = dlogit * r;
       const double dssq = -dlogit * a * r * r * r / (2.0 * (double)d);
       for (int64_t k = 0; k < d; ++k) {

@@ -1,0 +1,185 @@
+"""The C ABI without a GPU: the library loads, exports every declared symbol,
+rejects bad arguments with its status codes before touching a device, and its
+planner makes the documented dispatch decisions."""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import re
+
+import pytest
+import torch
+
+from switchyard import _lib
+
+HEADER = pathlib.Path(__file__).resolve().parents[1] / "include" / "switchyard.h"
+OK, NULL, SHAPE, DTYPE, WORKSPACE, STRIDE, DEVICE, OP = 0, -1, -2, -3, -4, -5, -6, -7
+BF16, F16, F32 = 2, 1, 0
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(sy_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    names = declared_functions()
+    assert len(names) >= 14, names
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in switchyard.h but not exported"
+    assert set(names) == set(_lib.SIGNATURES), "ctypes table and header disagree"
+
+
+def test_abi_version_and_error_strings():
+    lib = _lib.lib()
+    assert lib.sy_abi_version() == 1
+    for code in (OK, NULL, SHAPE, DTYPE, WORKSPACE, STRIDE, DEVICE, OP):
+        assert lib.sy_strerror(code)
+    assert b"NULL" in lib.sy_strerror(NULL)
+    assert b"unknown" in lib.sy_strerror(-99)
+
+
+def _p(x: int | None):
+    return None if x is None else ctypes.c_void_p(x)
+
+
+FAKE = 0x1000  # never dereferenced: every call below fails validation first
+
+
+@pytest.mark.parametrize(
+    "args,code",
+    [
+        ((None, FAKE, FAKE, None, 9, 16, 2048, 16 * 2048, BF16, BF16), NULL),
+        ((FAKE, FAKE, FAKE, None, 0, 16, 2048, 16 * 2048, BF16, BF16), SHAPE),
+        ((FAKE, FAKE, FAKE, None, 9, 16, 0, 0, BF16, BF16), SHAPE),
+        ((FAKE, FAKE, FAKE, None, 9, -1, 2048, 0, BF16, BF16), SHAPE),
+        ((FAKE, FAKE, FAKE, None, 9, 16, 2048, 16 * 2048, 7, BF16), DTYPE),
+        ((FAKE, FAKE, FAKE, None, 9, 16, 2048, 16 * 2048, BF16, -1), DTYPE),
+        ((FAKE, FAKE, FAKE, None, 9, 16, 2048, 100, BF16, BF16), STRIDE),
+    ],
+)
+def test_forward_rejects_bad_arguments_before_device_work(args, code):
+    v, w, out, stats, n, t, d, stride, vt, wt = args
+    rc = _lib.lib().sy_fwd(_p(v), _p(w), _p(out), _p(stats), n, t, d, stride, vt, wt, 1e-6, None)
+    assert rc == code
+
+
+def test_forward_with_no_tokens_is_a_no_op():
+    # Empty tensors have NULL data pointers; nothing is launched.
+    assert _lib.lib().sy_fwd(None, None, None, None, 9, 0, 2048, 0, BF16, BF16, 1e-6, None) == OK
+
+
+def test_backward_and_batched_reject_bad_arguments():
+    lib = _lib.lib()
+    # dw is always written, so it is required even with no tokens
+    assert lib.sy_bwd(None, None, None, None, None, None, None, 0, 9, 0, 2048, 0, BF16, BF16, 1e-6, None) == NULL
+    assert lib.sy_bwd(_p(FAKE), _p(FAKE), None, None, _p(FAKE), _p(FAKE), _p(FAKE), 1 << 20,
+                      9, 16, 2048, 16 * 2048, BF16, BF16, 1e-6, None) == NULL
+    assert lib.sy_bwd_main(_p(FAKE), _p(FAKE), _p(FAKE), None, _p(FAKE), _p(FAKE), 1 << 20,
+                           0, 16, 2048, 16 * 2048, BF16, BF16, 1e-6, None) == SHAPE
+    assert lib.sy_fwd_batched(_p(FAKE), _p(FAKE), _p(FAKE), 9, 0, 16, 2048, 16 * 2048, BF16, 1e-6, None) == SHAPE
+    assert lib.sy_fwd_batched(None, _p(FAKE), _p(FAKE), 9, 4, 16, 2048, 16 * 2048, BF16, 1e-6, None) == NULL
+    assert lib.sy_sol(_p(FAKE), _p(FAKE), 9, 16, 2048, 16 * 2048, 9, None) == DTYPE
+    assert lib.sy_dw_reduce(None, 4, 2048, _p(FAKE), BF16, None) == NULL
+    assert lib.sy_dw_reduce(_p(FAKE), 4, 0, _p(FAKE), BF16, None) == SHAPE
+    assert lib.sy_bw_probe(3, _p(FAKE), _p(FAKE), 1024, None) == OP
+    assert lib.sy_bw_probe(0, _p(FAKE), _p(FAKE), 1000, None) == SHAPE
+    assert lib.sy_bw_probe(2, None, _p(FAKE), 1024, None) == NULL
+    assert lib.sy_bwd_workspace_bytes(0, 16, 2048, BF16, BF16) == SHAPE
+    assert lib.sy_bwd_workspace_bytes(9, 16, 2048, 5, BF16) == DTYPE
+    assert lib.sy_bwd_workspace_bytes(9, 0, 2048, BF16, BF16) == 0
+    assert lib.sy_bwd_partial_rows(9, 0, 2048, BF16, BF16, 1, 1) == 0
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-device status")
+def test_device_queries_report_missing_device():
+    lib = _lib.lib()
+    assert lib.sy_bwd_workspace_bytes(9, 4096, 2048, BF16, BF16) == DEVICE
+    info = (ctypes.c_int32 * 4)()
+    assert lib.sy_kernel_info(0, 9, 4096, 2048, BF16, BF16, info) in (DEVICE, OK)
+
+
+def test_probe_grid_is_bounded():
+    lib = _lib.lib()
+    assert lib.sy_probe_grid(16) == 1
+    assert lib.sy_probe_grid(1 << 30) == 32768
+    assert lib.sy_probe_grid(1 << 20) == 64
+    assert lib.sy_probe_grid(0) == 1
+
+
+# --------------------------------------------------------------------------
+# Planner (pure host arithmetic)
+# --------------------------------------------------------------------------
+
+
+def plan(op, n, d, dt=torch.bfloat16, **kw):
+    return _lib.plan(op, n, d, dt, **kw)
+
+
+def test_representative_shape_is_register_resident_everywhere():
+    for op in (_lib.OP_FWD, _lib.OP_BWD, _lib.OP_SOL):
+        assert plan(op, 9, 2048)["family_name"] == "resident"
+    assert plan(_lib.OP_BATCHED, 9, 2048, n_q=8)["family_name"] == "resident"
+
+
+@pytest.mark.parametrize("n,d", [(9, 4096), (16, 2048), (9, 8192), (16, 4096), (4, 1024), (1, 256)])
+def test_sweep_shapes_stay_resident_in_both_directions(n, d):
+    assert plan(_lib.OP_FWD, n, d)["family_name"] == "resident"
+    assert plan(_lib.OP_BWD, n, d)["family_name"] == "resident"
+
+
+def test_tiles_cover_the_row_exactly_once():
+    for n in (1, 2, 9, 16):
+        for d in (64, 128, 512, 1024, 1536, 2048, 4096, 8192):
+            for dt, ce in ((torch.bfloat16, 8), (torch.float16, 8), (torch.float32, 4)):
+                for op in (_lib.OP_FWD, _lib.OP_BWD):
+                    p = plan(op, n, d, dt)
+                    if p["family_name"] in ("resident", "chunked"):
+                        assert p["elems_per_chunk"] == ce
+                        cover = 64 * p["waves_per_token"] * p["chunks_per_lane"] * ce
+                        assert cover >= d and cover < 2 * d + 64 * ce, (n, d, dt, op, p)
+                        if p["family_name"] == "resident":
+                            assert p["rows_per_tile"] >= n
+
+
+def test_large_n_forward_uses_online_chunks_and_backward_the_generic_kernel():
+    f = plan(_lib.OP_FWD, 33, 512)
+    assert f["family_name"] == "chunked" and f["n_chunks"] == 3
+    assert plan(_lib.OP_FWD, 17, 2048)["family_name"] == "chunked"
+    assert plan(_lib.OP_BWD, 17, 2048)["family_name"] == "generic"
+
+
+def test_unaligned_rows_and_mixed_dtypes_take_the_generic_kernels():
+    assert plan(_lib.OP_FWD, 3, 777)["family_name"] == "generic"
+    assert plan(_lib.OP_BWD, 5, 63)["family_name"] == "generic"
+    assert plan(_lib.OP_FWD, 9, 2048, aligned=False)["family_name"] == "generic"
+    assert plan(_lib.OP_FWD, 9, 2048, w_dtype=torch.float32)["family_name"] == "generic"
+    assert plan(_lib.OP_BATCHED, 3, 777, n_q=2)["family_name"] == "per_query"
+
+
+def test_batched_query_cap():
+    assert plan(_lib.OP_BATCHED, 9, 2048, n_q=16)["family_name"] == "resident"
+    assert plan(_lib.OP_BATCHED, 9, 2048, n_q=17)["family_name"] == "per_query"
+
+
+def test_backward_never_takes_a_four_chunk_tile():
+    for n in (1, 2, 4, 9):
+        for d in (512, 1024, 2048, 4096, 8192):
+            p = plan(_lib.OP_BWD, n, d)
+            if p["family_name"] == "resident":
+                assert p["chunks_per_lane"] <= 2
+                assert p["block_threads"] == 512
+                assert p["tokens_per_block"] * p["waves_per_token"] == 8
+
+
+def test_planner_rejects_bad_input():
+    p = _lib.Plan()
+    lib = _lib.lib()
+    assert lib.sy_plan_for(9, 9, 0, 2048, BF16, BF16, 1, ctypes.byref(p)) == OP
+    assert lib.sy_plan_for(0, 0, 0, 2048, BF16, BF16, 1, ctypes.byref(p)) == SHAPE
+    assert lib.sy_plan_for(2, 9, 0, 2048, BF16, BF16, 1, ctypes.byref(p)) == SHAPE
+    assert lib.sy_plan_for(0, 9, 0, 2048, 3, BF16, 1, ctypes.byref(p)) == DTYPE
+    assert lib.sy_plan_for(0, 9, 0, 2048, BF16, BF16, 1, None) == NULL
+    assert lib.sy_plan_for(0, 5000, 0, 7, BF16, BF16, 1, ctypes.byref(p)) == SHAPE
