@@ -25,6 +25,10 @@ Modes:
   python bench.py --kernel {fwd,bwd,reduce,sol,copy} --iters K
                                                 run one kernel K times (for rocprofv3)
   python bench.py --summarize DIR --title T     rocprofv3 CSV -> markdown summary
+  python bench.py --sweep                       BASELINE configs 3-4: batched Q=8 and the
+                                                N / T / D sweeps (fwd, fwd+bwd), JSON lines
+  python bench.py --model [--model-scale S]     config 5: decoder training step, standard vs
+                                                AttnRes (framework) vs AttnRes (HIP), JSON line
   python bench.py --traffic FETCH_DIR WRITE_DIR --json-out F
                                                 rocprofv3 --pmc runs of --kernel all ->
                                                 calibrated HBM bytes per launch (JSON)
@@ -76,6 +80,12 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--summarize", type=pathlib.Path, default=None)
     ap.add_argument("--title", default="")
     ap.add_argument("--json-out", type=pathlib.Path, default=None)
+    ap.add_argument("--sweep", action="store_true")
+    ap.add_argument("--model", action="store_true")
+    ap.add_argument("--model-scale", default="1.3B", choices=["1.3B", "small"])
+    ap.add_argument("--model-batch", type=int, default=4)
+    ap.add_argument("--model-seq", type=int, default=2048)
+    ap.add_argument("--model-reps", type=int, default=10)
     ap.add_argument("--traffic", nargs=2, type=pathlib.Path, default=None, metavar=("FETCH_DIR", "WRITE_DIR"))
     return ap.parse_args()
 
@@ -384,8 +394,147 @@ def traffic_mode(args):
     print(line)
 
 
+SWEEP_SHAPES = (
+    [("n-sweep", n, 1, 4096, 2048) for n in (2, 4, 9, 16)]
+    + [("t-sweep", 9, 1, t, 2048) for t in (512, 1024, 2048, 4096, 8192, 16384)]
+    + [("d-sweep", 9, 4, 4096, d) for d in (1024, 2048, 4096)]
+)
+
+
+def sweep_mode(args):
+    """Configs 3 and 4 of BASELINE.json: one JSON line per shape."""
+    import torch
+
+    from switchyard import _lib, harness
+    from switchyard.reference import attn_res_batched_bytes, attn_res_min_bytes, attn_res_train_bytes
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lib, st = _lib.lib(), _lib.stream_ptr(dev)
+    P = Workload._p
+    gen = torch.Generator(device=dev).manual_seed(0)
+    for name, n, b, t, d in SWEEP_SHAPES:
+        nt = b * t
+        slab = nt * d * 2
+        rot = max(2, min(6, int((3 << 30) // ((2 * n + 3) * slab))))
+        sets = []
+        for _ in range(rot):
+            v = torch.randn(n, b, t, d, device=dev, generator=gen).to(torch.bfloat16)
+            sets.append(dict(v=v, g=torch.randn(b, t, d, device=dev, generator=gen).to(torch.bfloat16),
+                             out=torch.empty(b, t, d, device=dev, dtype=torch.bfloat16),
+                             stats=torch.empty(2, n, nt, device=dev), dv=torch.empty_like(v),
+                             dw=torch.empty(d, device=dev, dtype=torch.bfloat16)))
+        w = (0.5 * torch.randn(d, device=dev, generator=gen)).to(torch.bfloat16)
+        ws_bytes = int(lib.sy_bwd_workspace_bytes(n, nt, d, 2, 2))
+        ws = torch.empty(max(1, ws_bytes // 4), device=dev)
+
+        def fwd(s):
+            _lib.check(lib.sy_fwd(P(s["v"]), P(w), P(s["out"]), P(s["stats"]), n, nt, d, nt * d, 2, 2, 1e-6, st), "sy_fwd")
+
+        def bwd(s):
+            _lib.check(lib.sy_bwd(P(s["v"]), P(w), P(s["g"]), P(s["stats"]), P(s["dv"]), P(s["dw"]), P(ws),
+                                  ws_bytes, n, nt, d, nt * d, 2, 2, 1e-6, st), "sy_bwd")
+
+        iters = max(20, min(200, int(2e5 / (n * t * b * d / 1e4))))
+        f_ms = harness.time_loop([lambda s=s: fwd(s) for s in sets], device=dev, iters=iters)
+        fb_ms = harness.time_loop([lambda s=s: (fwd(s), bwd(s)) for s in sets], device=dev, iters=iters)
+        fb = attn_res_train_bytes(n, b, t, d)
+        fw = attn_res_min_bytes(n, b, t, d)
+        rec = {"sweep": name, "N": n, "B": b, "T": t, "D": d, "dtype": "bf16", "rotating_sets": rot,
+               "fwd_us": round(f_ms * 1e3, 2), "fwd_gbps": round(fw / f_ms / 1e6, 1),
+               "fwd_frac_hbm_peak": round(fw / f_ms / 1e6 / HBM_PEAK_GBPS, 4),
+               "fwd_bwd_us": round(fb_ms * 1e3, 2), "fwd_bwd_gbps": round(fb / fb_ms / 1e6, 1),
+               "fwd_bwd_frac_hbm_peak": round(fb / fb_ms / 1e6 / HBM_PEAK_GBPS, 4)}
+        print(json.dumps(rec), flush=True)
+        del sets, ws
+        torch.cuda.empty_cache()
+    # Config 3: batched, Q=8 queries sharing one read of v.
+    n, b, t, d, q = 9, 1, 4096, 2048, 8
+    nt = b * t
+    sets = [dict(v=torch.randn(n, b, t, d, device=dev, generator=gen).to(torch.bfloat16),
+                 out=torch.empty(q, b, t, d, device=dev, dtype=torch.bfloat16)) for _ in range(6)]
+    gq = torch.Generator().manual_seed(1)
+    queries = (0.5 * torch.randn(q, d, generator=gq)).to(torch.bfloat16).to(dev)
+
+    def batched(s):
+        _lib.check(lib.sy_fwd_batched(P(s["v"]), P(queries), P(s["out"]), n, q, nt, d, nt * d, 2, 1e-6, st),
+                   "sy_fwd_batched")
+
+    ms = harness.time_loop([lambda s=s: batched(s) for s in sets], device=dev, iters=100)
+    nbytes = attn_res_batched_bytes(n, q, b, t, d)
+    print(json.dumps({"sweep": "batched", "N": n, "B": b, "T": t, "D": d, "Q": q, "dtype": "bf16",
+                      "us": round(ms * 1e3, 2), "gbps": round(nbytes / ms / 1e6, 1),
+                      "frac_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBPS, 4),
+                      "reference_rtx_pro_6000_us": 198.7}), flush=True)
+
+
+MODEL_SCALES = {
+    "1.3B": dict(vocab_size=32000, d_model=2048, n_layers=24, n_heads=16, d_ff=5632, n_blocks=8, max_seq_len=4096),
+    "small": dict(vocab_size=4096, d_model=512, n_layers=8, n_heads=8, d_ff=1408, n_blocks=4, max_seq_len=512),
+}
+
+
+def model_mode(args):
+    """Config 5: tokens/s of a bf16 AdamW training step (reference bench/bench_model.py)."""
+    import torch
+
+    from switchyard import harness
+    from switchyard.model import ModelConfig, Transformer
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    bsz, seq = args.model_batch, args.model_seq
+    variants = [("standard", "arena"), ("attnres", "arena"), ("switchyard", "arena"), ("switchyard", "stack")]
+    out = {"metric": "decoder training step tokens/s (config 5)", "scale": args.model_scale,
+           "config": MODEL_SCALES[args.model_scale], "batch": bsz, "seq": seq, "dtype": "bf16",
+           "data": "uniform-random token ids, random-init weights (seed 0)", "variants": []}
+    for residual, sources in variants:
+        torch.manual_seed(0)
+        cfg = ModelConfig(**MODEL_SCALES[args.model_scale], residual=residual, sources=sources)
+        model = Transformer(cfg).to(device=dev, dtype=torch.bfloat16)
+        opt = torch.optim.AdamW(model.parameters(), lr=1e-6)
+        idx = torch.randint(0, cfg.vocab_size, (bsz, seq), device=dev)
+        tgt = torch.randint(0, cfg.vocab_size, (bsz, seq), device=dev)
+
+        def step():
+            model.zero_grad(set_to_none=True)
+            model(idx, tgt)[1].backward()
+            opt.step()
+
+        def fwd():
+            with torch.no_grad():
+                return model(idx, tgt)[1]
+
+        t_step = harness.measure_latency(step, device=dev, warmup=3, reps=args.model_reps, flush=False)
+        t_fwd = harness.measure_latency(fwd, device=dev, warmup=2, reps=args.model_reps, flush=False)
+        torch.cuda.reset_peak_memory_stats(dev)
+        step()
+        torch.cuda.synchronize(dev)
+        rec = {"variant": residual if residual == "standard" else f"{residual}/{sources}",
+               "params": model.param_counts()["total"], "step_ms": round(t_step.median_ms, 3),
+               "forward_nograd_ms": round(t_fwd.median_ms, 3),
+               "tokens_per_s": round(bsz * seq / (t_step.median_ms * 1e-3), 1),
+               "peak_memory_gib": round(torch.cuda.max_memory_allocated(dev) / 2**30, 2)}
+        out["variants"].append(rec)
+        log(json.dumps(rec))
+        del model, opt
+        torch.cuda.empty_cache()
+    base = out["variants"][0]["step_ms"]
+    for r in out["variants"][1:]:
+        r["share_of_step_vs_control"] = round(1 - base / r["step_ms"], 4)
+    out["reference_rtx_pro_6000"] = {"standard_tok_s": 19101, "switchyard_arena_tok_s": 16918,
+                                     "note": "reference README.md:82-84, vocab 32768"}
+    print(json.dumps(out), flush=True)
+
+
 def main() -> None:
     args = parse_args()
+    if args.sweep:
+        sweep_mode(args)
+        return
+    if args.model:
+        model_mode(args)
+        return
     if args.traffic is not None:
         traffic_mode(args)
         return
