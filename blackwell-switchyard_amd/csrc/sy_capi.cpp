@@ -60,6 +60,28 @@ int bwd_grid(const sy_plan& p, int64_t n_tok, int dtype, bool stats, int* grid) 
   return SY_OK;
 }
 
+// Persistent grid of the batched backward (also sizes its workspace).
+int bwd_batched_grid(const sy_plan& p, int64_t n_tok, int dtype, int* grid) {
+  int cus = 0;
+  hipError_t e = cu_count(&cus);
+  if (e != hipSuccess) return e == hipErrorNoDevice ? SY_ERR_DEVICE : (int)e;
+  int per_cu = 2;
+  if (p.family != SY_FAMILY_GENERIC) {
+    KernelRes r;
+    e = dtype == SY_BF16 ? bwd_batched_vec_resources_bf16(p, &r)
+        : dtype == SY_F16 ? bwd_batched_vec_resources_f16(p, &r)
+                          : bwd_batched_vec_resources_f32(p, &r);
+    if (e != hipSuccess) return (int)e;
+    per_cu = r.blocks_per_cu;
+  }
+  const int64_t slots = (n_tok + p.tokens_per_block - 1) / p.tokens_per_block;
+  int64_t g = (int64_t)cus * per_cu;
+  if (g > slots) g = slots;
+  if (g < 1) g = 1;
+  *grid = (int)g;
+  return SY_OK;
+}
+
 hipError_t fwd_vec(const sy_plan& p, const FwdArgs& a, hipStream_t s) {
   if (a.v_dtype == SY_BF16) return launch_fwd_vec_bf16(p, a, s, nullptr);
   if (a.v_dtype == SY_F16) return launch_fwd_vec_f16(p, a, s, nullptr);
@@ -82,12 +104,44 @@ hipError_t bwd_vec(const sy_plan& p, const BwdArgs& a, int grid, hipStream_t s) 
 }
 
 // Shared argument checks for v-shaped inputs.
-int check_common(int64_t n_src, int64_t n_tok, int64_t d, int64_t src_stride, int v_dtype,
-                 int w_dtype) {
+int check_sizes(int64_t n_src, int64_t n_tok, int64_t d, int v_dtype, int w_dtype) {
   if (!valid_dtype(v_dtype) || !valid_dtype(w_dtype)) return SY_ERR_DTYPE;
   if (n_src < 1 || d < 1 || n_tok < 0) return SY_ERR_SHAPE;
   if (n_src > 0x7fffffff || d > 0x7fffffff / 16 || n_tok > ((int64_t)1 << 40)) return SY_ERR_SHAPE;
+  return SY_OK;
+}
+int check_common(int64_t n_src, int64_t n_tok, int64_t d, int64_t src_stride, int v_dtype,
+                 int w_dtype) {
+  const int rc = check_sizes(n_src, n_tok, d, v_dtype, w_dtype);
+  if (rc != SY_OK) return rc;
   if (n_src > 1 && src_stride < n_tok * d) return SY_ERR_STRIDE;
+  return SY_OK;
+}
+
+// Row tables. `rows_ok` reports whether every row start is 16-byte aligned so
+// that the vector kernels may be used (token rows then stay aligned when
+// D * itemsize is a multiple of 16, checked by the callers).
+RowTable stacked_rows(const void* base, int64_t n_src, int64_t stride, int dtype, bool* rows_ok) {
+  RowTable t{};
+  const int64_t sb = stride * esize(dtype);
+  for (int n = 0; n < kTableRows && n < n_src; ++n)
+    t.p[n] = const_cast<char*>(static_cast<const char*>(base)) + n * sb;
+  t.stride_bytes = sb;
+  *rows_ok = al16(base) && sb % 16 == 0;
+  return t;
+}
+
+// A caller's list of N row pointers (N <= kTableRows). SY_ERR_NULL if any is NULL.
+int listed_rows(const void* const* rows, int64_t n_src, RowTable* t, bool* rows_ok) {
+  *t = RowTable{};
+  *rows_ok = true;
+  if (rows == nullptr) return SY_ERR_NULL;
+  if (n_src > kTableRows) return SY_ERR_SHAPE;
+  for (int n = 0; n < n_src; ++n) {
+    if (rows[n] == nullptr) return SY_ERR_NULL;
+    t->p[n] = const_cast<void*>(rows[n]);
+    *rows_ok = *rows_ok && al16(rows[n]);
+  }
   return SY_OK;
 }
 
@@ -118,6 +172,110 @@ hipError_t cu_count(int* out) {
 
 using namespace sy;
 
+namespace {
+
+bool vec_rows(bool rows_ok, int64_t d, int dtype) { return rows_ok && (d * esize(dtype)) % 16 == 0; }
+
+// Forward of the operator (normalize = 1) or of attn_with_stats (normalize = 0
+// with m_out/l_out) over any row table. Sizes are already checked.
+int fwd_impl(const RowTable& v, bool v_ok, const void* w, void* out, float* stats, float* m_out,
+             float* l_out, int normalize, int64_t n_src, int64_t n_tok, int64_t d, int v_dtype,
+             int w_dtype, float eps, hipStream_t s) {
+  const bool aligned = vec_rows(v_ok, d, v_dtype) && al16(w) && al16(out);
+  sy_plan p;
+  const int rc = make_plan(SY_OP_FWD, n_src, 0, d, v_dtype, w_dtype, aligned, &p);
+  if (rc != SY_OK) return rc;
+  apply_tile_override(SY_OP_FWD, n_src, d, &p);
+  if (n_tok == 0) return SY_OK;
+  const FwdArgs a{v,      w,       out,     stats,   m_out, l_out, normalize, (int)n_src,
+                  n_tok,  (int)d,  v_dtype, w_dtype, eps};
+  return status(p.family == SY_FAMILY_GENERIC ? launch_fwd_generic(a, s) : fwd_vec(p, a, s));
+}
+
+// Main backward kernel over row tables: dv and the fp32 dw partials.
+// *rows_out receives the partial row count (the persistent grid).
+int bwd_main_impl(const RowTable& v, bool v_ok, const void* w, const void* g, const float* stats,
+                  const float* gm, const float* gl, const RowTable& dv, bool dv_ok,
+                  void* workspace, int64_t workspace_bytes, int64_t n_src, int64_t n_tok,
+                  int64_t d, int v_dtype, int w_dtype, float eps, hipStream_t s, int* rows_out) {
+  *rows_out = 0;
+  if (n_tok == 0) return SY_OK;
+  const bool aligned = vec_rows(v_ok && dv_ok, d, v_dtype) && al16(w) && al16(g) && al16(workspace);
+  sy_plan p;
+  int rc = make_plan(SY_OP_BWD, n_src, 0, d, v_dtype, w_dtype, aligned, &p);
+  if (rc != SY_OK) return rc;
+  apply_tile_override(SY_OP_BWD, n_src, d, &p);
+  int grid = 0;
+  rc = bwd_grid(p, n_tok, v_dtype, stats != nullptr, &grid);
+  if (rc != SY_OK) return rc;
+  if (workspace == nullptr || workspace_bytes < (int64_t)grid * d * (int64_t)sizeof(float))
+    return SY_ERR_WORKSPACE;
+  const BwdArgs a{v,  w,          g,     stats,  gm,      gl,      dv,  (float*)workspace,
+                  (int)n_src, n_tok, (int)d, v_dtype, w_dtype, eps};
+  const hipError_t e =
+      p.family == SY_FAMILY_GENERIC ? launch_bwd_generic(a, grid, s) : bwd_vec(p, a, grid, s);
+  if (e != hipSuccess) return (int)e;
+  *rows_out = grid;
+  return SY_OK;
+}
+
+// Main kernel then the fixed-order dw reduction (dw is written even with no
+// tokens: it is then zero).
+int bwd_impl(const RowTable& v, bool v_ok, const void* w, const void* g, const float* stats,
+             const float* gm, const float* gl, const RowTable& dv, bool dv_ok, void* dw,
+             void* workspace, int64_t workspace_bytes, int64_t n_src, int64_t n_tok, int64_t d,
+             int v_dtype, int w_dtype, float eps, hipStream_t s) {
+  int rows = 0;
+  const int rc = bwd_main_impl(v, v_ok, w, g, stats, gm, gl, dv, dv_ok, workspace, workspace_bytes,
+                               n_src, n_tok, d, v_dtype, w_dtype, eps, s, &rows);
+  if (rc != SY_OK) return rc;
+  return status(launch_dw_reduce((const float*)workspace, rows, (int)d, dw, w_dtype, s));
+}
+
+// Batched forward: the resident kernel, else one forward launch per query
+// written straight into out[q] (and m_out[q], l_out[q]).
+int batched_impl(const RowTable& v, bool v_ok, const void* q, void* out, float* m_out, float* l_out,
+                 int normalize, int64_t n_src, int64_t n_q, int64_t n_tok, int64_t d, int dtype,
+                 float eps, hipStream_t s) {
+  const bool aligned = vec_rows(v_ok, d, dtype) && al16(q) && al16(out);
+  sy_plan p;
+  int rc = make_plan(SY_OP_BATCHED, n_src, n_q, d, dtype, dtype, aligned, &p);
+  if (rc != SY_OK) return rc;
+  apply_tile_override(SY_OP_BATCHED, n_src, d, &p);
+  if (n_tok == 0) return SY_OK;
+  if (p.family == SY_FAMILY_RESIDENT) {
+    const BatchedArgs a{v,          q,        out,   m_out,  l_out, normalize,
+                        (int)n_src, (int)n_q, n_tok, (int)d, dtype, eps};
+    return status(batched_vec(p, a, s));
+  }
+  const int64_t es = esize(dtype);
+  for (int64_t k = 0; k < n_q; ++k) {
+    rc = fwd_impl(v, v_ok, (const char*)q + k * d * es, (char*)out + k * n_tok * d * es, nullptr,
+                  m_out ? m_out + k * n_tok : nullptr, l_out ? l_out + k * n_tok : nullptr,
+                  normalize, n_src, n_tok, d, dtype, dtype, eps, s);
+    if (rc != SY_OK) return rc;
+  }
+  return SY_OK;
+}
+
+// Stacked-layout source table with the stride check already done.
+RowTable stacked(const void* v, int64_t n_src, int64_t stride, int dtype, bool* ok) {
+  return stacked_rows(v, n_src, stride, dtype, ok);
+}
+
+// Pointer-list source table: sizes checked, N within the table.
+int listed(const void* const* rows, int64_t n_src, int64_t n_tok, RowTable* t, bool* ok) {
+  if (n_src > kTableRows) return SY_ERR_SHAPE;
+  if (n_tok == 0) {
+    *t = RowTable{};
+    *ok = true;
+    return SY_OK;
+  }
+  return listed_rows(rows, n_src, t, ok);
+}
+
+}  // namespace
+
 extern "C" {
 
 int sy_abi_version(void) { return SY_ABI_VERSION; }
@@ -131,18 +289,39 @@ int sy_fwd(const void* v, const void* w, void* out, float* stats, int64_t n_src,
            int64_t d, int64_t src_stride, int v_dtype, int w_dtype, float eps, void* stream) {
   // Empty tensors have NULL data pointers; with no tokens nothing is touched.
   if (n_tok != 0 && (v == nullptr || w == nullptr || out == nullptr)) return SY_ERR_NULL;
-  int rc = check_common(n_src, n_tok, d, src_stride, v_dtype, w_dtype);
+  const int rc = check_common(n_src, n_tok, d, src_stride, v_dtype, w_dtype);
   if (rc != SY_OK) return rc;
-  const bool aligned = rows_aligned(v, src_stride, v_dtype) && rows_aligned(v, d, v_dtype) &&
-                       al16(w) && al16(out) && (d * esize(v_dtype)) % 16 == 0;
-  sy_plan p;
-  rc = make_plan(SY_OP_FWD, n_src, 0, d, v_dtype, w_dtype, aligned, &p);
+  bool ok = false;
+  const RowTable t = stacked(v, n_src, src_stride, v_dtype, &ok);
+  return fwd_impl(t, ok, w, out, stats, nullptr, nullptr, 1, n_src, n_tok, d, v_dtype, w_dtype, eps,
+                  (hipStream_t)stream);
+}
+
+int sy_fwd_table(const void* const* v_rows, const void* w, void* out, float* stats, int64_t n_src,
+                 int64_t n_tok, int64_t d, int v_dtype, int w_dtype, float eps, void* stream) {
+  if (n_tok != 0 && (v_rows == nullptr || w == nullptr || out == nullptr)) return SY_ERR_NULL;
+  int rc = check_sizes(n_src, n_tok, d, v_dtype, w_dtype);
   if (rc != SY_OK) return rc;
-  apply_tile_override(SY_OP_FWD, n_src, d, &p);
-  if (n_tok == 0) return SY_OK;
-  const FwdArgs a{v, w, out, stats, (int)n_src, n_tok, (int)d, src_stride, v_dtype, w_dtype, eps};
-  const hipStream_t s = (hipStream_t)stream;
-  return status(p.family == SY_FAMILY_GENERIC ? launch_fwd_generic(a, s) : fwd_vec(p, a, s));
+  RowTable t;
+  bool ok = false;
+  rc = listed(v_rows, n_src, n_tok, &t, &ok);
+  if (rc != SY_OK) return rc;
+  return fwd_impl(t, ok, w, out, stats, nullptr, nullptr, 1, n_src, n_tok, d, v_dtype, w_dtype, eps,
+                  (hipStream_t)stream);
+}
+
+int sy_attn_with_stats(const void* v, const void* w, void* o, float* m, float* l, float* stats,
+                       int64_t n_src, int64_t n_tok, int64_t d, int64_t src_stride, int v_dtype,
+                       int w_dtype, float eps, void* stream) {
+  if (n_tok != 0 &&
+      (v == nullptr || w == nullptr || o == nullptr || m == nullptr || l == nullptr))
+    return SY_ERR_NULL;
+  const int rc = check_common(n_src, n_tok, d, src_stride, v_dtype, w_dtype);
+  if (rc != SY_OK) return rc;
+  bool ok = false;
+  const RowTable t = stacked(v, n_src, src_stride, v_dtype, &ok);
+  return fwd_impl(t, ok, w, o, stats, m, l, 0, n_src, n_tok, d, v_dtype, w_dtype, eps,
+                  (hipStream_t)stream);
 }
 
 int sy_sol(const void* v, void* out, int64_t n_src, int64_t n_tok, int64_t d, int64_t src_stride,
@@ -150,20 +329,22 @@ int sy_sol(const void* v, void* out, int64_t n_src, int64_t n_tok, int64_t d, in
   if (n_tok != 0 && (v == nullptr || out == nullptr)) return SY_ERR_NULL;
   int rc = check_common(n_src, n_tok, d, src_stride, dtype, dtype);
   if (rc != SY_OK) return rc;
-  const bool aligned = rows_aligned(v, src_stride, dtype) && rows_aligned(v, d, dtype) &&
-                       al16(out) && (d * esize(dtype)) % 16 == 0;
+  bool ok = false;
+  const RowTable t = stacked(v, n_src, src_stride, dtype, &ok);
+  const bool aligned = vec_rows(ok, d, dtype) && al16(out);
   sy_plan p;
   rc = make_plan(SY_OP_SOL, n_src, 0, d, dtype, dtype, aligned, &p);
   if (rc != SY_OK) return rc;
   apply_tile_override(SY_OP_SOL, n_src, d, &p);
   if (n_tok == 0) return SY_OK;
-  const FwdArgs a{v, nullptr, out, nullptr, (int)n_src, n_tok, (int)d, src_stride, dtype, dtype, 0.0f};
+  const FwdArgs a{t,     nullptr, out,   nullptr, nullptr, nullptr, 1, (int)n_src,
+                  n_tok, (int)d,  dtype, dtype,   0.0f};
   const hipStream_t s = (hipStream_t)stream;
   return status(p.family == SY_FAMILY_GENERIC ? launch_sol_generic(a, s) : sol_vec(p, a, s));
 }
 
 int64_t sy_bwd_workspace_bytes(int64_t n_src, int64_t n_tok, int64_t d, int v_dtype, int w_dtype) {
-  int rc = check_common(n_src, n_tok, d, n_tok * d, v_dtype, w_dtype);
+  int rc = check_sizes(n_src, n_tok, d, v_dtype, w_dtype);
   if (rc != SY_OK) return rc;
   if (n_tok == 0) return 0;
   // The vector plan assumes aligned buffers; a misaligned call falls back to
@@ -186,62 +367,78 @@ int64_t sy_bwd_workspace_bytes(int64_t n_src, int64_t n_tok, int64_t d, int v_dt
   return g * d * (int64_t)sizeof(float);
 }
 
-// Main backward kernel: dv and the fp32 dw partials. *rows_out receives the
-// partial row count (the persistent grid).
-static int bwd_main(const void* v, const void* w, const void* grad_out, const float* stats,
-                    void* dv, void* workspace, int64_t workspace_bytes, int64_t n_src,
-                    int64_t n_tok, int64_t d, int64_t src_stride, int v_dtype, int w_dtype,
-                    float eps, hipStream_t s, int* rows_out) {
-  *rows_out = 0;
-  if (n_tok != 0 && (v == nullptr || w == nullptr || grad_out == nullptr || dv == nullptr))
-    return SY_ERR_NULL;
-  int rc = check_common(n_src, n_tok, d, src_stride, v_dtype, w_dtype);
-  if (rc != SY_OK || n_tok == 0) return rc;
-  const bool aligned = rows_aligned(v, src_stride, v_dtype) && rows_aligned(v, d, v_dtype) &&
-                       al16(w) && al16(grad_out) && al16(dv) && al16(workspace) &&
-                       (d * esize(v_dtype)) % 16 == 0;
-  sy_plan p;
-  rc = make_plan(SY_OP_BWD, n_src, 0, d, v_dtype, w_dtype, aligned, &p);
-  if (rc != SY_OK) return rc;
-  apply_tile_override(SY_OP_BWD, n_src, d, &p);
-  int grid = 0;
-  rc = bwd_grid(p, n_tok, v_dtype, stats != nullptr, &grid);
-  if (rc != SY_OK) return rc;
-  if (workspace == nullptr || workspace_bytes < (int64_t)grid * d * (int64_t)sizeof(float))
-    return SY_ERR_WORKSPACE;
-  const BwdArgs a{v, w, grad_out, stats, dv, nullptr, (float*)workspace, (int)n_src, n_tok, (int)d,
-                  src_stride, v_dtype, w_dtype, eps};
-  hipError_t e = p.family == SY_FAMILY_GENERIC ? launch_bwd_generic(a, grid, s)
-                                               : bwd_vec(p, a, grid, s);
-  if (e != hipSuccess) return (int)e;
-  *rows_out = grid;
-  return SY_OK;
-}
-
 int sy_bwd(const void* v, const void* w, const void* grad_out, const float* stats, void* dv,
            void* dw, void* workspace, int64_t workspace_bytes, int64_t n_src, int64_t n_tok,
            int64_t d, int64_t src_stride, int v_dtype, int w_dtype, float eps, void* stream) {
-  // dw is written even when there are no tokens (it is then zero).
   if (dw == nullptr) return SY_ERR_NULL;
-  const hipStream_t s = (hipStream_t)stream;
-  int rows = 0;
-  const int rc = bwd_main(v, w, grad_out, stats, dv, workspace, workspace_bytes, n_src, n_tok, d,
-                          src_stride, v_dtype, w_dtype, eps, s, &rows);
+  if (n_tok != 0 && (v == nullptr || w == nullptr || grad_out == nullptr || dv == nullptr))
+    return SY_ERR_NULL;
+  const int rc = check_common(n_src, n_tok, d, src_stride, v_dtype, w_dtype);
   if (rc != SY_OK) return rc;
-  return status(launch_dw_reduce((const float*)workspace, rows, (int)d, dw, w_dtype, s));
+  bool vok = false, dok = false;
+  const RowTable tv = stacked(v, n_src, src_stride, v_dtype, &vok);
+  const RowTable td = stacked(dv, n_src, n_tok * d, v_dtype, &dok);
+  return bwd_impl(tv, vok, w, grad_out, stats, nullptr, nullptr, td, dok, dw, workspace,
+                  workspace_bytes, n_src, n_tok, d, v_dtype, w_dtype, eps, (hipStream_t)stream);
+}
+
+int sy_bwd_table(const void* const* v_rows, const void* w, const void* grad_out,
+                 const float* stats, void* const* dv_rows, void* dw, void* workspace,
+                 int64_t workspace_bytes, int64_t n_src, int64_t n_tok, int64_t d, int v_dtype,
+                 int w_dtype, float eps, void* stream) {
+  if (dw == nullptr) return SY_ERR_NULL;
+  if (n_tok != 0 &&
+      (v_rows == nullptr || w == nullptr || grad_out == nullptr || dv_rows == nullptr))
+    return SY_ERR_NULL;
+  int rc = check_sizes(n_src, n_tok, d, v_dtype, w_dtype);
+  if (rc != SY_OK) return rc;
+  RowTable tv, td;
+  bool vok = false, dok = false;
+  rc = listed(v_rows, n_src, n_tok, &tv, &vok);
+  if (rc != SY_OK) return rc;
+  rc = listed(reinterpret_cast<const void* const*>(dv_rows), n_src, n_tok, &td, &dok);
+  if (rc != SY_OK) return rc;
+  return bwd_impl(tv, vok, w, grad_out, stats, nullptr, nullptr, td, dok, dw, workspace,
+                  workspace_bytes, n_src, n_tok, d, v_dtype, w_dtype, eps, (hipStream_t)stream);
+}
+
+int sy_attn_with_stats_bwd(const void* v, const void* w, const void* grad_o, const float* grad_m,
+                           const float* grad_l, const float* stats, void* dv, void* dw,
+                           void* workspace, int64_t workspace_bytes, int64_t n_src, int64_t n_tok,
+                           int64_t d, int64_t src_stride, int v_dtype, int w_dtype, float eps,
+                           void* stream) {
+  if (dw == nullptr) return SY_ERR_NULL;
+  if (n_tok != 0 && (v == nullptr || w == nullptr || grad_o == nullptr || grad_m == nullptr ||
+                     grad_l == nullptr || dv == nullptr))
+    return SY_ERR_NULL;
+  const int rc = check_common(n_src, n_tok, d, src_stride, v_dtype, w_dtype);
+  if (rc != SY_OK) return rc;
+  bool vok = false, dok = false;
+  const RowTable tv = stacked(v, n_src, src_stride, v_dtype, &vok);
+  const RowTable td = stacked(dv, n_src, n_tok * d, v_dtype, &dok);
+  return bwd_impl(tv, vok, w, grad_o, stats, grad_m, grad_l, td, dok, dw, workspace,
+                  workspace_bytes, n_src, n_tok, d, v_dtype, w_dtype, eps, (hipStream_t)stream);
 }
 
 int sy_bwd_main(const void* v, const void* w, const void* grad_out, const float* stats, void* dv,
                 void* workspace, int64_t workspace_bytes, int64_t n_src, int64_t n_tok, int64_t d,
                 int64_t src_stride, int v_dtype, int w_dtype, float eps, void* stream) {
+  if (n_tok != 0 && (v == nullptr || w == nullptr || grad_out == nullptr || dv == nullptr))
+    return SY_ERR_NULL;
+  const int rc = check_common(n_src, n_tok, d, src_stride, v_dtype, w_dtype);
+  if (rc != SY_OK) return rc;
+  bool vok = false, dok = false;
+  const RowTable tv = stacked(v, n_src, src_stride, v_dtype, &vok);
+  const RowTable td = stacked(dv, n_src, n_tok * d, v_dtype, &dok);
   int rows = 0;
-  return bwd_main(v, w, grad_out, stats, dv, workspace, workspace_bytes, n_src, n_tok, d,
-                  src_stride, v_dtype, w_dtype, eps, (hipStream_t)stream, &rows);
+  return bwd_main_impl(tv, vok, w, grad_out, stats, nullptr, nullptr, td, dok, workspace,
+                       workspace_bytes, n_src, n_tok, d, v_dtype, w_dtype, eps,
+                       (hipStream_t)stream, &rows);
 }
 
 int64_t sy_bwd_partial_rows(int64_t n_src, int64_t n_tok, int64_t d, int v_dtype, int w_dtype,
                             int aligned, int has_stats) {
-  int rc = check_common(n_src, n_tok, d, n_tok * d, v_dtype, w_dtype);
+  int rc = check_sizes(n_src, n_tok, d, v_dtype, w_dtype);
   if (rc != SY_OK) return rc;
   if (n_tok == 0) return 0;
   sy_plan p;
@@ -256,7 +453,7 @@ int64_t sy_bwd_partial_rows(int64_t n_src, int64_t n_tok, int64_t d, int v_dtype
 int sy_kernel_info(int op, int64_t n_src, int64_t n_tok, int64_t d, int v_dtype, int w_dtype,
                    int32_t out[4]) {
   if (out == nullptr) return SY_ERR_NULL;
-  int rc = check_common(n_src, n_tok, d, n_tok * d, v_dtype, w_dtype);
+  int rc = check_sizes(n_src, n_tok, d, v_dtype, w_dtype);
   if (rc != SY_OK) return rc;
   if (op != SY_OP_FWD && op != SY_OP_BWD) return SY_ERR_OP;
   sy_plan p;
@@ -268,8 +465,8 @@ int sy_kernel_info(int op, int64_t n_src, int64_t n_tok, int64_t d, int v_dtype,
   KernelRes r{0, 0, 0, 0};
   hipError_t e;
   if (op == SY_OP_FWD) {
-    const FwdArgs a{nullptr, nullptr, nullptr, nullptr, (int)n_src, n_tok, (int)d, n_tok * d,
-                    v_dtype, w_dtype, 0.0f};
+    const FwdArgs a{RowTable{}, nullptr, nullptr, nullptr, nullptr, nullptr, 1, (int)n_src,
+                    n_tok,      (int)d,  v_dtype, w_dtype, 0.0f};
     e = v_dtype == SY_BF16 ? launch_fwd_vec_bf16(p, a, nullptr, &r)
         : v_dtype == SY_F16 ? launch_fwd_vec_f16(p, a, nullptr, &r)
                             : launch_fwd_vec_f32(p, a, nullptr, &r);
@@ -300,29 +497,135 @@ int sy_fwd_batched(const void* v, const void* queries, void* out, int64_t n_src,
                    int64_t n_tok, int64_t d, int64_t src_stride, int dtype, float eps,
                    void* stream) {
   if (n_tok != 0 && (v == nullptr || queries == nullptr || out == nullptr)) return SY_ERR_NULL;
-  int rc = check_common(n_src, n_tok, d, src_stride, dtype, dtype);
+  const int rc = check_common(n_src, n_tok, d, src_stride, dtype, dtype);
   if (rc != SY_OK) return rc;
   if (n_q < 1 || n_q > 0x7fffffff) return SY_ERR_SHAPE;
-  const bool aligned = rows_aligned(v, src_stride, dtype) && rows_aligned(v, d, dtype) &&
-                       al16(queries) && al16(out) && (d * esize(dtype)) % 16 == 0;
-  sy_plan p;
-  rc = make_plan(SY_OP_BATCHED, n_src, n_q, d, dtype, dtype, aligned, &p);
+  bool ok = false;
+  const RowTable t = stacked(v, n_src, src_stride, dtype, &ok);
+  return batched_impl(t, ok, queries, out, nullptr, nullptr, 1, n_src, n_q, n_tok, d, dtype, eps,
+                      (hipStream_t)stream);
+}
+
+int sy_fwd_batched_table(const void* const* v_rows, const void* queries, void* out, int64_t n_src,
+                         int64_t n_q, int64_t n_tok, int64_t d, int dtype, float eps,
+                         void* stream) {
+  if (n_tok != 0 && (v_rows == nullptr || queries == nullptr || out == nullptr)) return SY_ERR_NULL;
+  int rc = check_sizes(n_src, n_tok, d, dtype, dtype);
   if (rc != SY_OK) return rc;
-  apply_tile_override(SY_OP_BATCHED, n_src, d, &p);
-  if (n_tok == 0) return SY_OK;
-  const hipStream_t s = (hipStream_t)stream;
-  if (p.family == SY_FAMILY_RESIDENT) {
-    const BatchedArgs a{v, queries, out, (int)n_src, (int)n_q, n_tok, (int)d, src_stride, dtype, eps};
-    return status(batched_vec(p, a, s));
-  }
-  // One forward launch per query, written straight into out[s].
-  const int64_t es = esize(dtype);
-  for (int64_t q = 0; q < n_q; ++q) {
-    rc = sy_fwd(v, (const char*)queries + q * d * es, (char*)out + q * n_tok * d * es, nullptr,
-                n_src, n_tok, d, src_stride, dtype, dtype, eps, stream);
+  if (n_q < 1 || n_q > 0x7fffffff) return SY_ERR_SHAPE;
+  RowTable t;
+  bool ok = false;
+  rc = listed(v_rows, n_src, n_tok, &t, &ok);
+  if (rc != SY_OK) return rc;
+  return batched_impl(t, ok, queries, out, nullptr, nullptr, 1, n_src, n_q, n_tok, d, dtype, eps,
+                      (hipStream_t)stream);
+}
+
+int sy_batched_with_stats(const void* v, const void* queries, void* o, float* m, float* l,
+                          int64_t n_src, int64_t n_q, int64_t n_tok, int64_t d, int64_t src_stride,
+                          int dtype, float eps, void* stream) {
+  if (n_tok != 0 && (v == nullptr || queries == nullptr || o == nullptr || m == nullptr ||
+                     l == nullptr))
+    return SY_ERR_NULL;
+  const int rc = check_common(n_src, n_tok, d, src_stride, dtype, dtype);
+  if (rc != SY_OK) return rc;
+  if (n_q < 1 || n_q > 0x7fffffff) return SY_ERR_SHAPE;
+  bool ok = false;
+  const RowTable t = stacked(v, n_src, src_stride, dtype, &ok);
+  return batched_impl(t, ok, queries, o, m, l, 0, n_src, n_q, n_tok, d, dtype, eps,
+                      (hipStream_t)stream);
+}
+
+int64_t sy_bwd_batched_workspace_bytes(int64_t n_src, int64_t n_q, int64_t n_tok, int64_t d,
+                                       int dtype) {
+  int rc = check_sizes(n_src, n_tok, d, dtype, dtype);
+  if (rc != SY_OK) return rc;
+  if (n_q < 1 || n_q > 0x7fffffff) return SY_ERR_SHAPE;
+  if (n_tok == 0) return 0;
+  int64_t g = 0;
+  for (int aligned : {1, 0}) {
+    sy_plan p;
+    rc = make_plan(SY_OP_BWD_BATCHED, n_src, n_q, d, dtype, dtype, aligned, &p);
     if (rc != SY_OK) return rc;
+    int gi = 0;
+    rc = bwd_batched_grid(p, n_tok, dtype, &gi);
+    if (rc != SY_OK) return rc;
+    if (gi > g) g = gi;
   }
-  return SY_OK;
+  return g * n_q * d * (int64_t)sizeof(float);
+}
+
+int sy_bwd_batched(const void* v, const void* queries, const void* grad_out, void* dv, void* dq,
+                   void* workspace, int64_t workspace_bytes, int64_t n_src, int64_t n_q,
+                   int64_t n_tok, int64_t d, int64_t src_stride, int dtype, float eps,
+                   void* stream) {
+  if (dq == nullptr) return SY_ERR_NULL;
+  if (n_tok != 0 &&
+      (v == nullptr || queries == nullptr || grad_out == nullptr || dv == nullptr))
+    return SY_ERR_NULL;
+  int rc = check_common(n_src, n_tok, d, src_stride, dtype, dtype);
+  if (rc != SY_OK) return rc;
+  if (n_q < 1 || n_q > 0x7fffffff || n_q * d > 0x7fffffff / 16) return SY_ERR_SHAPE;
+  const hipStream_t s = (hipStream_t)stream;
+  bool vok = false, dok = false;
+  const RowTable tv = stacked(v, n_src, src_stride, dtype, &vok);
+  const RowTable td = stacked(dv, n_src, n_tok * d, dtype, &dok);
+  const bool aligned = vec_rows(vok && dok, d, dtype) && al16(queries) && al16(grad_out) &&
+                       al16(workspace);
+  sy_plan p;
+  rc = make_plan(SY_OP_BWD_BATCHED, n_src, n_q, d, dtype, dtype, aligned, &p);
+  if (rc != SY_OK) return rc;
+  int grid = 0;
+  if (n_tok != 0) {
+    rc = bwd_batched_grid(p, n_tok, dtype, &grid);
+    if (rc != SY_OK) return rc;
+    if (workspace == nullptr || workspace_bytes < (int64_t)grid * n_q * d * (int64_t)sizeof(float))
+      return SY_ERR_WORKSPACE;
+    const BwdBatchedArgs a{tv,         queries,    grad_out, td,     (float*)workspace,
+                           (int)n_src, (int)n_q,   n_tok,    (int)d, dtype,
+                           eps};
+    hipError_t e;
+    if (p.family == SY_FAMILY_GENERIC) {
+      e = launch_bwd_batched_generic(a, grid, s);
+    } else {
+      e = dtype == SY_BF16 ? launch_bwd_batched_vec_bf16(p, a, grid, s)
+          : dtype == SY_F16 ? launch_bwd_batched_vec_f16(p, a, grid, s)
+                            : launch_bwd_batched_vec_f32(p, a, grid, s);
+    }
+    if (e != hipSuccess) return (int)e;
+  }
+  // dq[s][c] = sum over the grid's partial rows, fixed order (zero without tokens).
+  return status(launch_dw_reduce((const float*)workspace, grid, (int)(n_q * d), dq, dtype, s));
+}
+
+int sy_merge_stats(const void* o1, const float* m1, const float* l1, const void* o2,
+                   const float* m2, const float* l2, void* o, float* m, float* l, int64_t n_tok,
+                   int64_t d, int dtype, void* stream) {
+  if (!valid_dtype(dtype)) return SY_ERR_DTYPE;
+  if (n_tok < 0 || n_tok > ((int64_t)1 << 40) || d < 1 || d > 0x7fffffff / 16) return SY_ERR_SHAPE;
+  if (n_tok == 0) return SY_OK;
+  if (!o1 || !m1 || !l1 || !o2 || !m2 || !l2 || !o || !m || !l) return SY_ERR_NULL;
+  const bool vec = al16(o1) && al16(o2) && al16(o) && (d * esize(dtype)) % 16 == 0;
+  const MergeArgs a{o1, m1, l1, o2, m2, l2, o, m, l, n_tok, (int)d};
+  return status(launch_merge(a, dtype, vec, (hipStream_t)stream));
+}
+
+int sy_merge_stats_bwd(const void* o1, const float* m1, const float* l1, const void* o2,
+                       const float* m2, const float* l2, const void* grad_o, const float* grad_m,
+                       const float* grad_l, void* do1, float* dm1, float* dl1, void* do2,
+                       float* dm2, float* dl2, int64_t n_tok, int64_t d, int dtype,
+                       void* stream) {
+  if (!valid_dtype(dtype)) return SY_ERR_DTYPE;
+  if (n_tok < 0 || n_tok > ((int64_t)1 << 40) || d < 1 || d > 0x7fffffff / 16) return SY_ERR_SHAPE;
+  if (n_tok == 0) return SY_OK;
+  if (!o1 || !m1 || !l1 || !o2 || !m2 || !l2 || !grad_o || !grad_m || !grad_l || !do1 || !dm1 ||
+      !dl1 || !do2 || !dm2 || !dl2)
+    return SY_ERR_NULL;
+  const bool vec = al16(o1) && al16(o2) && al16(grad_o) && al16(do1) && al16(do2) &&
+                   (d * esize(dtype)) % 16 == 0;
+  const MergeBwdArgs a{o1,  m1,  l1,  o2,  m2,  l2,  grad_o, grad_m,  grad_l,
+                       do1, dm1, dl1, do2, dm2, dl2, n_tok,  (int)d};
+  return status(launch_merge_bwd(a, dtype, vec, (hipStream_t)stream));
 }
 
 int64_t sy_probe_grid(int64_t bytes) {

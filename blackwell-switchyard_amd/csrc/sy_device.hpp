@@ -24,6 +24,25 @@ struct BF16 { using storage = uint16_t; static constexpr int code = 2; static co
 struct F16  { using storage = uint16_t; static constexpr int code = 1; static constexpr int ce = 8; };
 struct F32  { using storage = float;    static constexpr int code = 0; static constexpr int ce = 4; };
 
+// Where the N source rows of a token start (and, for dv, the N gradient rows).
+// Row n of token t is at row_of(table, n) + t*D. Rows n < kTableRows come from
+// p[n]; rows beyond are p[0] + n*stride_bytes, the stacked [N][n_tok][D]
+// layout. A stacked caller fills p[n] = base + n*stride; a caller with one
+// tensor per source fills p[0..N) directly and needs N <= kTableRows. The table
+// travels in the kernel arguments, so the resident kernels (compile-time n)
+// read each row pointer with one scalar load.
+constexpr int kTableRows = 16;
+struct RowTable {
+  void* p[kTableRows];
+  int64_t stride_bytes;
+};
+
+template <class S>
+__host__ __device__ __forceinline__ S* row_of(const RowTable& t, int n) {
+  return n < kTableRows ? static_cast<S*>(t.p[n])
+                        : reinterpret_cast<S*>(static_cast<char*>(t.p[0]) + (int64_t)n * t.stride_bytes);
+}
+
 // Buffer resource word 3 for gfx9-family raw buffers (32-bit dword format).
 constexpr int kRsrcFlags = 0x00020000;
 

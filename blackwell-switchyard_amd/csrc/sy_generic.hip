@@ -52,9 +52,9 @@ __device__ float block_max(float x, float* scr) {
 // Pass 1 for one token: per-row (sum of squares, query dot[, grad dot]) for
 // every row, written to ss[], qd[] and gd[] in LDS. Rows go in groups of 8 so
 // a thread carries 16-24 partial sums.
-__device__ void row_scalars(const void* v, const void* w, const void* g, int n_src, int64_t tok,
-                            int d, int64_t src_stride, int vt, int wt, float* ss, float* qd,
-                            float* gd, float* scr) {
+__device__ void row_scalars(const RowTable& v, const void* w, const void* g, int n_src,
+                            int64_t tok, int d, int vt, int wt, float* ss, float* qd, float* gd,
+                            float* scr) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -69,7 +69,7 @@ __device__ void row_scalars(const void* v, const void* w, const void* g, int n_s
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         if (g0 + r < n_src) {
-          const float x = load_elem(v, (int64_t)(g0 + r) * src_stride + tok * d + k, vt);
+          const float x = load_elem(row_of<const char>(v, g0 + r), tok * d + k, vt);
           a[r] = fmaf(x, x, a[r]);
           b[r] = fmaf(x, wk, b[r]);
           c[r] = fmaf(x, gk, c[r]);
@@ -108,16 +108,17 @@ __device__ void row_scalars(const void* v, const void* w, const void* g, int n_s
 
 // LDS layout (floats): [0, n) lg, [n, 2n) ss/r, [2n, 3n) gd, then 257 scratch.
 __global__ void __launch_bounds__(kBlock)
-k_fwd_generic(const void* __restrict__ v, const void* __restrict__ w, void* __restrict__ out,
-              float* __restrict__ stats, int n_src, int64_t n_tok, int d, int64_t src_stride,
-              int vt, int wt, float eps, float inv_d) {
+k_fwd_generic(const RowTable v, const void* __restrict__ w, void* __restrict__ out,
+              float* __restrict__ stats, float* __restrict__ m_out, float* __restrict__ l_out,
+              int normalize, int n_src, int64_t n_tok, int d, int vt, int wt, float eps,
+              float inv_d) {
   extern __shared__ float sh[];
   float* lg = sh;
   float* ss = sh + n_src;
   float* scr = sh + 2 * n_src;
   const int tid = threadIdx.x;
   const int64_t tok = blockIdx.x;
-  row_scalars(v, w, nullptr, n_src, tok, d, src_stride, vt, wt, ss, lg, nullptr, scr);
+  row_scalars(v, w, nullptr, n_src, tok, d, vt, wt, ss, lg, nullptr, scr);
 
   float m = -INFINITY;
   for (int n = tid; n < n_src; n += kBlock) {
@@ -130,7 +131,11 @@ k_fwd_generic(const void* __restrict__ v, const void* __restrict__ w, void* __re
   float l = 0.0f;
   for (int n = tid; n < n_src; n += kBlock) l += expf(lg[n] - m);
   l = block_sum(l, scr);
-  const float inv_l = 1.0f / l;
+  const float inv_l = normalize ? 1.0f / l : 1.0f;
+  if (m_out != nullptr && tid == 0) {
+    m_out[tok] = m;
+    l_out[tok] = l;
+  }
   if (stats) {
     for (int n = tid; n < n_src; n += kBlock) {
       stats[(int64_t)n * n_tok + tok] = lg[n];
@@ -143,28 +148,29 @@ k_fwd_generic(const void* __restrict__ v, const void* __restrict__ w, void* __re
   for (int k = tid; k < d; k += kBlock) {
     float acc = 0.0f;
     for (int n = 0; n < n_src; ++n)
-      acc = fmaf(lg[n], load_elem(v, (int64_t)n * src_stride + tok * d + k, vt), acc);
+      acc = fmaf(lg[n], load_elem(row_of<const char>(v, n), tok * d + k, vt), acc);
     store_elem(out, tok * d + k, acc, vt);
   }
 }
 
 __global__ void __launch_bounds__(kBlock)
-k_sol_generic(const void* __restrict__ v, void* __restrict__ out, int n_src, int64_t n_tok, int d,
-              int64_t src_stride, int vt) {
+k_sol_generic(const RowTable v, void* __restrict__ out, int n_src, int64_t n_tok, int d, int vt) {
   const int64_t tok = blockIdx.x;
   for (int k = threadIdx.x; k < d; k += kBlock) {
     float acc = 0.0f;
-    for (int n = 0; n < n_src; ++n) acc += load_elem(v, (int64_t)n * src_stride + tok * d + k, vt);
+    for (int n = 0; n < n_src; ++n) acc += load_elem(row_of<const char>(v, n), tok * d + k, vt);
     store_elem(out, tok * d + k, acc, vt);
   }
 }
 
 // Persistent over tokens; workgroup b accumulates its dw contribution in its
-// own fp32 row partial[b][:] (no other workgroup touches it).
+// own fp32 row partial[b][:] (no other workgroup touches it). gm != nullptr
+// selects the gradient of the unnormalised (o, m, l) triple, as in k_bwd.
 __global__ void __launch_bounds__(kBlock)
-k_bwd_generic(const void* __restrict__ v, const void* __restrict__ w, const void* __restrict__ g,
-              void* __restrict__ dv, float* __restrict__ partial, int n_src, int64_t n_tok, int d,
-              int64_t src_stride, int vt, int wt, float eps, float inv_d) {
+k_bwd_generic(const RowTable v, const void* __restrict__ w, const void* __restrict__ g,
+              const float* __restrict__ gm, const float* __restrict__ gl, const RowTable dv,
+              float* __restrict__ partial, int n_src, int64_t n_tok, int d, int vt, int wt,
+              float eps, float inv_d) {
   extern __shared__ float sh[];
   float* al = sh;              // logit, then alpha
   float* da = sh + n_src;      // sum of squares, then r, then da
@@ -173,10 +179,9 @@ k_bwd_generic(const void* __restrict__ v, const void* __restrict__ w, const void
   const int tid = threadIdx.x;
   float* prow = partial + (int64_t)blockIdx.x * d;
   for (int k = tid; k < d; k += kBlock) prow[k] = 0.0f;
-  const int64_t dv_stride = n_tok * d;
 
   for (int64_t tok = blockIdx.x; tok < n_tok; tok += gridDim.x) {
-    row_scalars(v, w, g, n_src, tok, d, src_stride, vt, wt, da, al, gc, scr);
+    row_scalars(v, w, g, n_src, tok, d, vt, wt, da, al, gc, scr);
     float m = -INFINITY;
     for (int n = tid; n < n_src; n += kBlock) {
       const float r = rsqrtf(fmaf(da[n], inv_d, eps));
@@ -191,24 +196,41 @@ k_bwd_generic(const void* __restrict__ v, const void* __restrict__ w, const void
     for (int n = tid; n < n_src; n += kBlock)
       if (al[n] == m) first = fminf(first, (float)n);
     first = -block_max(-first, scr);
-    const float gref = gc[min((int)first, n_src - 1)];
-    float l = 0.0f, sp = 0.0f;
-    for (int n = tid; n < n_src; n += kBlock) {
-      const float p = expf(al[n] - m);
-      l += p;
-      sp = fmaf(p, gc[n] - gref, sp);
-    }
-    l = block_sum(l, scr);
-    sp = block_sum(sp, scr);
-    const float inv_l = 1.0f / l;
-    const float sdev = sp * inv_l;
-    for (int n = tid; n < n_src; n += kBlock) {
-      const float lgn = al[n], r = da[n];
-      const float a = expf(lgn - m) * inv_l;
-      const float dlogit = a * ((gc[n] - gref) - sdev);
-      al[n] = a;
-      da[n] = dlogit * r;
-      gc[n] = -dlogit * lgn * r * r * inv_d;
+    const int top = min((int)first, n_src - 1);
+    if (gm == nullptr) {
+      const float gref = gc[top];
+      float l = 0.0f, sp = 0.0f;
+      for (int n = tid; n < n_src; n += kBlock) {
+        const float p = expf(al[n] - m);
+        l += p;
+        sp = fmaf(p, gc[n] - gref, sp);
+      }
+      l = block_sum(l, scr);
+      sp = block_sum(sp, scr);
+      const float inv_l = 1.0f / l;
+      const float sdev = sp * inv_l;
+      for (int n = tid; n < n_src; n += kBlock) {
+        const float lgn = al[n], r = da[n];
+        const float a = expf(lgn - m) * inv_l;
+        const float dlogit = a * ((gc[n] - gref) - sdev);
+        al[n] = a;
+        da[n] = dlogit * r;
+        gc[n] = -dlogit * lgn * r * r * inv_d;
+      }
+    } else {
+      const float glv = gl[tok], gmv = gm[tok];
+      float other = 0.0f;
+      for (int n = tid; n < n_src; n += kBlock)
+        if (n != top) other = fmaf(expf(al[n] - m), gc[n] + glv, other);
+      other = block_sum(other, scr);
+      for (int n = tid; n < n_src; n += kBlock) {
+        const float lgn = al[n], r = da[n];
+        const float p = expf(lgn - m);
+        const float dlogit = n == top ? gmv - other : p * (gc[n] + glv);
+        al[n] = p;
+        da[n] = dlogit * r;
+        gc[n] = -dlogit * lgn * r * r * inv_d;
+      }
     }
     __syncthreads();
     for (int k = tid; k < d; k += kBlock) {
@@ -216,12 +238,97 @@ k_bwd_generic(const void* __restrict__ v, const void* __restrict__ w, const void
       const float wk = load_elem(w, k, wt);
       float dwk = 0.0f;
       for (int n = 0; n < n_src; ++n) {
-        const float x = load_elem(v, (int64_t)n * src_stride + tok * d + k, vt);
-        store_elem(dv, (int64_t)n * dv_stride + tok * d + k,
+        const float x = load_elem(row_of<const char>(v, n), tok * d + k, vt);
+        store_elem(row_of<char>(dv, n), tok * d + k,
                    fmaf(gc[n], x, fmaf(da[n], wk, al[n] * gk)), vt);
         dwk = fmaf(da[n], x, dwk);
       }
       prow[k] += dwk;
+    }
+    __syncthreads();
+  }
+}
+
+// Batched backward for the shapes the register tile does not take (see
+// k_bwd_batched for the algebra). Persistent over tokens, one workgroup per
+// token; per token and query the row scalars go to LDS, then one pass over D
+// writes dv and adds the workgroup's dq contribution to its own fp32 rows
+// partial[b][s][:]. LDS floats: al[S*N], da[S*N], c[N], r[N], ss/qd/gd[N]
+// and the 257-float reduction scratch (bwd_batched_generic_lds).
+__global__ void __launch_bounds__(kBlock)
+k_bwd_batched_generic(const RowTable v, const void* __restrict__ q, const void* __restrict__ g,
+                      const RowTable dv, float* __restrict__ partial, int n_src, int n_q,
+                      int64_t n_tok, int d, int vt, float eps, float inv_d) {
+  extern __shared__ float sh[];
+  const int nn = n_src, sn = n_q * n_src;
+  float* al = sh;
+  float* da = sh + sn;
+  float* cc = sh + 2 * sn;
+  float* rr = cc + nn;
+  float* ss = rr + nn;
+  float* qd = ss + nn;
+  float* gd = qd + nn;
+  float* scr = gd + nn;
+  const int tid = threadIdx.x;
+  const int64_t es = vt == 0 ? 4 : 2;
+  float* prow = partial + (int64_t)blockIdx.x * n_q * d;
+  for (int64_t k = tid; k < (int64_t)n_q * d; k += kBlock) prow[k] = 0.0f;
+
+  for (int64_t tok = blockIdx.x; tok < n_tok; tok += gridDim.x) {
+    for (int n = tid; n < nn; n += kBlock) cc[n] = 0.0f;
+    for (int s = 0; s < n_q; ++s) {
+      const char* qs = static_cast<const char*>(q) + (int64_t)s * d * es;
+      const char* gs = static_cast<const char*>(g) + (int64_t)s * n_tok * d * es;
+      row_scalars(v, qs, gs, nn, tok, d, vt, vt, ss, qd, gd, scr);
+      float m = -INFINITY;
+      for (int n = tid; n < nn; n += kBlock) {
+        const float r = rsqrtf(fmaf(ss[n], inv_d, eps));
+        rr[n] = r;
+        qd[n] *= r;  // logit
+        m = fmaxf(m, qd[n]);
+      }
+      m = block_max(m, scr);
+      float first = (float)nn;
+      for (int n = tid; n < nn; n += kBlock)
+        if (qd[n] == m) first = fminf(first, (float)n);
+      first = -block_max(-first, scr);
+      const float gref = gd[min((int)first, nn - 1)];
+      float l = 0.0f, sp = 0.0f;
+      for (int n = tid; n < nn; n += kBlock) {
+        const float p = expf(qd[n] - m);
+        l += p;
+        sp = fmaf(p, gd[n] - gref, sp);
+      }
+      l = block_sum(l, scr);
+      sp = block_sum(sp, scr);
+      const float inv_l = 1.0f / l;
+      const float sdev = sp * inv_l;
+      for (int n = tid; n < nn; n += kBlock) {
+        const float a = expf(qd[n] - m) * inv_l;
+        const float dlogit = a * ((gd[n] - gref) - sdev);
+        al[s * nn + n] = a;
+        da[s * nn + n] = dlogit * rr[n];
+        cc[n] = fmaf(-dlogit * qd[n], rr[n] * rr[n] * inv_d, cc[n]);
+      }
+      __syncthreads();
+    }
+    for (int k = tid; k < d; k += kBlock) {
+      for (int n = 0; n < nn; ++n) {
+        const float x = load_elem(row_of<const char>(v, n), tok * d + k, vt);
+        float acc = cc[n] * x;
+        for (int s = 0; s < n_q; ++s) {
+          const float gk = load_elem(g, ((int64_t)s * n_tok + tok) * d + k, vt);
+          const float qk = load_elem(q, (int64_t)s * d + k, vt);
+          acc = fmaf(al[s * nn + n], gk, fmaf(da[s * nn + n], qk, acc));
+        }
+        store_elem(row_of<char>(dv, n), tok * d + k, acc, vt);
+      }
+      for (int s = 0; s < n_q; ++s) {
+        float u = 0.0f;
+        for (int n = 0; n < nn; ++n)
+          u = fmaf(da[s * nn + n], load_elem(row_of<const char>(v, n), tok * d + k, vt), u);
+        prow[(int64_t)s * d + k] += u;
+      }
     }
     __syncthreads();
   }
@@ -305,22 +412,29 @@ k_probe_copy(const i32x4_t* __restrict__ src, i32x4_t* __restrict__ dst, int64_t
 hipError_t launch_fwd_generic(const FwdArgs& a, hipStream_t s) {
   const size_t lds = (size_t)(2 * a.n_src + 257) * sizeof(float);
   hipLaunchKernelGGL(k_fwd_generic, dim3((unsigned)a.n_tok), dim3(kBlock), lds, s, a.v, a.w, a.out,
-                     a.stats, a.n_src, a.n_tok, a.d, a.src_stride, a.v_dtype, a.w_dtype, a.eps,
-                     1.0f / (float)a.d);
+                     a.stats, a.m_out, a.l_out, a.normalize, a.n_src, a.n_tok, a.d, a.v_dtype,
+                     a.w_dtype, a.eps, 1.0f / (float)a.d);
   return hipGetLastError();
 }
 
 hipError_t launch_sol_generic(const FwdArgs& a, hipStream_t s) {
   hipLaunchKernelGGL(k_sol_generic, dim3((unsigned)a.n_tok), dim3(kBlock), 0, s, a.v, a.out,
-                     a.n_src, a.n_tok, a.d, a.src_stride, a.v_dtype);
+                     a.n_src, a.n_tok, a.d, a.v_dtype);
   return hipGetLastError();
 }
 
 hipError_t launch_bwd_generic(const BwdArgs& a, int grid, hipStream_t s) {
   const size_t lds = (size_t)(3 * a.n_src + 257) * sizeof(float);
-  hipLaunchKernelGGL(k_bwd_generic, dim3(grid), dim3(kBlock), lds, s, a.v, a.w, a.g, a.dv,
-                     a.partial, a.n_src, a.n_tok, a.d, a.src_stride, a.v_dtype, a.w_dtype, a.eps,
+  hipLaunchKernelGGL(k_bwd_generic, dim3(grid), dim3(kBlock), lds, s, a.v, a.w, a.g, a.gm, a.gl,
+                     a.dv, a.partial, a.n_src, a.n_tok, a.d, a.v_dtype, a.w_dtype, a.eps,
                      1.0f / (float)a.d);
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd_batched_generic(const BwdBatchedArgs& a, int grid, hipStream_t s) {
+  const size_t lds = (size_t)bwd_batched_generic_lds(a.n_src, a.n_q);
+  hipLaunchKernelGGL(k_bwd_batched_generic, dim3(grid), dim3(kBlock), lds, s, a.v, a.q, a.g, a.dv,
+                     a.partial, a.n_src, a.n_q, a.n_tok, a.d, a.dtype, a.eps, 1.0f / (float)a.d);
   return hipGetLastError();
 }
 

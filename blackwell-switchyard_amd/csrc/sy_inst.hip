@@ -55,33 +55,33 @@ hipError_t SY_FN(launch_fwd_vec_)(const sy_plan& p, const FwdArgs& a, hipStream_
                                  KernelRes* info) {
   const float inv_d = 1.0f / (float)a.d;
   const bool res = p.family == SY_FAMILY_RESIDENT;
-#define X(W_, V_, N_)                                                                           \
-  if (tile_is(p, W_, V_, N_)) {                                                                 \
-    constexpr int kB = FwdGeom<W_>::kBlock, kT = FwdGeom<W_>::kTpb;                             \
-    if (res) {                                                                                  \
-      static const KernelRes kr = resources_of(k_fwd_res<T, W_, V_, N_>, kB);                   \
-      const int grid = launch_grid(kr, a.n_tok, kT);                                            \
-      if (info) {                                                                               \
-        *info = kr;                                                                             \
-        info->grid = grid;                                                                      \
-        return hipSuccess;                                                                      \
-      }                                                                                         \
-      const int n_iter = (int)cdiv(a.n_tok, (int64_t)grid * kT);                                \
-      hipLaunchKernelGGL((k_fwd_res<T, W_, V_, N_>), dim3(grid), dim3(kB), 0, s, (const St*)a.v, \
-                         (const St*)a.w, (St*)a.out, a.stats, a.n_src, a.n_tok, a.d,             \
-                         a.src_stride, a.eps, inv_d, n_iter);                                   \
-    } else {                                                                                    \
-      const int64_t grid = cdiv(a.n_tok, kT);                                                   \
-      if (info) {                                                                               \
-        *info = resources_of(k_fwd<T, W_, V_, N_>, kB);                                         \
-        info->grid = (int)grid;                                                                 \
-        return hipSuccess;                                                                      \
-      }                                                                                         \
-      hipLaunchKernelGGL((k_fwd<T, W_, V_, N_>), dim3((unsigned)grid), dim3(kB), 0, s,          \
-                         (const St*)a.v, (const St*)a.w, (St*)a.out, a.stats, a.n_src, a.n_tok, \
-                         a.d, a.src_stride, a.eps, inv_d);                                      \
-    }                                                                                           \
-    return hipGetLastError();                                                                   \
+#define X(W_, V_, N_)                                                                        \
+  if (tile_is(p, W_, V_, N_)) {                                                              \
+    constexpr int kB = FwdGeom<W_>::kBlock, kT = FwdGeom<W_>::kTpb;                          \
+    if (res) {                                                                               \
+      static const KernelRes kr = resources_of(k_fwd_res<T, W_, V_, N_>, kB);                \
+      const int grid = launch_grid(kr, a.n_tok, kT);                                         \
+      if (info) {                                                                            \
+        *info = kr;                                                                          \
+        info->grid = grid;                                                                   \
+        return hipSuccess;                                                                   \
+      }                                                                                      \
+      const int n_iter = (int)cdiv(a.n_tok, (int64_t)grid * kT);                             \
+      hipLaunchKernelGGL((k_fwd_res<T, W_, V_, N_>), dim3(grid), dim3(kB), 0, s, a.v,        \
+                         (const St*)a.w, (St*)a.out, a.stats, a.m_out, a.l_out, a.normalize, \
+                         a.n_src, a.n_tok, a.d, a.eps, inv_d, n_iter);                       \
+    } else {                                                                                 \
+      const int64_t grid = cdiv(a.n_tok, kT);                                                \
+      if (info) {                                                                            \
+        *info = resources_of(k_fwd<T, W_, V_, N_>, kB);                                      \
+        info->grid = (int)grid;                                                              \
+        return hipSuccess;                                                                   \
+      }                                                                                      \
+      hipLaunchKernelGGL((k_fwd<T, W_, V_, N_>), dim3((unsigned)grid), dim3(kB), 0, s, a.v,  \
+                         (const St*)a.w, (St*)a.out, a.stats, a.m_out, a.l_out, a.normalize, \
+                         a.n_src, a.n_tok, a.d, a.eps, inv_d);                               \
+    }                                                                                        \
+    return hipGetLastError();                                                                \
   }
   SY_TILES(X)
 #undef X
@@ -96,11 +96,10 @@ hipError_t SY_FN(launch_sol_vec_)(const sy_plan& p, const FwdArgs& a, hipStream_
     if (res) {                                                                                 \
       static const KernelRes kr = resources_of(k_sol_res<T, W_, V_, N_>, kB);                  \
       hipLaunchKernelGGL((k_sol_res<T, W_, V_, N_>), dim3(launch_grid(kr, a.n_tok, kT)),       \
-                         dim3(kB), 0, s, (const St*)a.v, (St*)a.out, a.n_src, a.n_tok, a.d,     \
-                         a.src_stride);                                                        \
+                         dim3(kB), 0, s, a.v, (St*)a.out, a.n_src, a.n_tok, a.d);              \
     } else {                                                                                   \
       hipLaunchKernelGGL((k_sol<T, W_, V_, N_>), dim3((unsigned)cdiv(a.n_tok, kT)), dim3(kB), 0, \
-                         s, (const St*)a.v, (St*)a.out, a.n_src, a.n_tok, a.d, a.src_stride);   \
+                         s, a.v, (St*)a.out, a.n_src, a.n_tok, a.d);                           \
     }                                                                                          \
     return hipGetLastError();                                                                  \
   }
@@ -115,8 +114,8 @@ hipError_t SY_FN(launch_batched_vec_)(const sy_plan& p, const BatchedArgs& a, hi
   if (tile_is(p, W_, V_, N_)) {                                                                  \
     constexpr int kB = FwdGeom<W_>::kBlock, kT = FwdGeom<W_>::kTpb;                              \
     hipLaunchKernelGGL((k_batched<T, W_, V_, N_>), dim3((unsigned)cdiv(a.n_tok, kT)), dim3(kB), 0, \
-                       s, (const St*)a.v, (const St*)a.q, (St*)a.out, a.n_src, a.n_q, a.n_tok,    \
-                       a.d, a.src_stride, a.eps, inv_d);                                         \
+                       s, a.v, (const St*)a.q, (St*)a.out, a.m_out, a.l_out, a.normalize,        \
+                       a.n_src, a.n_q, a.n_tok, a.d, a.eps, inv_d);                              \
     return hipGetLastError();                                                                    \
   }
   SY_TILES(X)
@@ -144,21 +143,54 @@ hipError_t SY_FN(launch_bwd_vec_)(const sy_plan& p, const BwdArgs& a, int grid, 
   const float inv_d = 1.0f / (float)a.d;
   const int64_t slots = (int64_t)grid * p.tokens_per_block;
   const int n_iter = (int)cdiv(a.n_tok, slots);
-#define X(W_, V_, N_)                                                                           \
-  if (tile_is(p, W_, V_, N_)) {                                                                 \
-    constexpr int kB = BwdGeom<W_>::kBlock;                                                     \
-    if (a.stats != nullptr) {                                                                   \
-      hipLaunchKernelGGL((k_bwd<T, W_, V_, N_, true>), dim3(grid), dim3(kB), 0, s,             \
-                         (const St*)a.v, (const St*)a.w, (const St*)a.g, a.stats, (St*)a.dv,     \
-                         a.partial, a.n_src, a.n_tok, a.d, a.src_stride, a.eps, inv_d, n_iter);  \
-    } else {                                                                                    \
-      hipLaunchKernelGGL((k_bwd<T, W_, V_, N_, false>), dim3(grid), dim3(kB), 0, s,            \
-                         (const St*)a.v, (const St*)a.w, (const St*)a.g, a.stats, (St*)a.dv,     \
-                         a.partial, a.n_src, a.n_tok, a.d, a.src_stride, a.eps, inv_d, n_iter);  \
-    }                                                                                           \
-    return hipGetLastError();                                                                   \
+#define X(W_, V_, N_)                                                                        \
+  if (tile_is(p, W_, V_, N_)) {                                                              \
+    constexpr int kB = BwdGeom<W_>::kBlock;                                                  \
+    if (a.stats != nullptr) {                                                                \
+      hipLaunchKernelGGL((k_bwd<T, W_, V_, N_, true>), dim3(grid), dim3(kB), 0, s, a.v,      \
+                         (const St*)a.w, (const St*)a.g, a.stats, a.gm, a.gl, a.dv,          \
+                         a.partial, a.n_src, a.n_tok, a.d, a.eps, inv_d, n_iter);            \
+    } else {                                                                                 \
+      hipLaunchKernelGGL((k_bwd<T, W_, V_, N_, false>), dim3(grid), dim3(kB), 0, s, a.v,     \
+                         (const St*)a.w, (const St*)a.g, a.stats, a.gm, a.gl, a.dv,          \
+                         a.partial, a.n_src, a.n_tok, a.d, a.eps, inv_d, n_iter);            \
+    }                                                                                        \
+    return hipGetLastError();                                                                \
   }
   SY_TILES(X)
+#undef X
+  return hipErrorInvalidConfiguration;
+}
+
+// Batched backward tiles: one chunk per lane, W waves per token, NR rows,
+// up to kBwdBatchedMaxQ queries.
+#define SY_BB_TILES(X) X(1, 4) X(1, 9) X(2, 4) X(2, 9) X(4, 4) X(4, 9) X(8, 4) X(8, 9)
+
+hipError_t SY_FN(bwd_batched_vec_resources_)(const sy_plan& p, KernelRes* out) {
+#define X(W_, N_)                                                                             \
+  if (tile_is(p, W_, 1, N_)) {                                                                \
+    static const KernelRes kr =                                                               \
+        resources_of(k_bwd_batched<T, W_, N_, (int)kBwdBatchedMaxQ>, FwdGeom<W_>::kBlock);     \
+    *out = kr;                                                                                \
+    return hipSuccess;                                                                        \
+  }
+  SY_BB_TILES(X)
+#undef X
+  return hipErrorInvalidConfiguration;
+}
+
+hipError_t SY_FN(launch_bwd_batched_vec_)(const sy_plan& p, const BwdBatchedArgs& a, int grid,
+                                         hipStream_t s) {
+  const float inv_d = 1.0f / (float)a.d;
+  const int n_iter = (int)cdiv(a.n_tok, (int64_t)grid * p.tokens_per_block);
+#define X(W_, N_)                                                                             \
+  if (tile_is(p, W_, 1, N_)) {                                                                \
+    hipLaunchKernelGGL((k_bwd_batched<T, W_, N_, (int)kBwdBatchedMaxQ>), dim3(grid),           \
+                       dim3(FwdGeom<W_>::kBlock), 0, s, a.v, (const St*)a.q, (const St*)a.g,  \
+                       a.dv, a.partial, a.n_src, a.n_q, a.n_tok, a.d, a.eps, inv_d, n_iter);  \
+    return hipGetLastError();                                                                 \
+  }
+  SY_BB_TILES(X)
 #undef X
   return hipErrorInvalidConfiguration;
 }

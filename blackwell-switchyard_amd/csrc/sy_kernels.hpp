@@ -71,12 +71,16 @@ __device__ __forceinline__ void cross_wave_sum(float (&vals)[G * NR], int groups
 // merges chunks with the online-softmax update (running max m, running sum l,
 // accumulator rescaled by exp(m_old - m_new)), which still reads v once.
 //
-// Optional stats: stats[n*n_tok + t] = logit, stats[(N+n)*n_tok + t] = r_n.
+// Optional outputs: stats[n*n_tok + t] = logit, stats[(N+n)*n_tok + t] = r_n;
+// m_out[t] = max logit and l_out[t] = sum_n exp(logit_n - m) (both or neither).
+// normalize = 0 stores the unnormalised o = sum_n exp(logit_n - m) v_n instead
+// of o / l (reference src/switchyard/reference.py:194-215, attn_with_stats).
 template <class T, int W, int VPL, int NR>
 __global__ void __launch_bounds__(FwdGeom<W>::kBlock)
-k_fwd(const typename T::storage* __restrict__ v, const typename T::storage* __restrict__ w,
-      typename T::storage* __restrict__ out, float* __restrict__ stats, int n_src,
-      int64_t n_tok, int d, int64_t src_stride, float eps, float inv_d) {
+k_fwd(const RowTable v, const typename T::storage* __restrict__ w,
+      typename T::storage* __restrict__ out, float* __restrict__ stats, float* __restrict__ m_out,
+      float* __restrict__ l_out, int normalize, int n_src, int64_t n_tok, int d, float eps,
+      float inv_d) {
   using S = typename T::storage;
   constexpr int CE = T::ce;
   constexpr int TPB = FwdGeom<W>::kTpb;
@@ -118,7 +122,7 @@ k_fwd(const typename T::storage* __restrict__ v, const typename T::storage* __re
 #pragma unroll
     for (int n = 0; n < NR; ++n) {
       if (n < rows) {
-        const auto r = make_rsrc(v + (int64_t)(c0 + n) * src_stride + tok * d, row_bytes);
+        const auto r = make_rsrc(row_of<const S>(v, c0 + n) + tok * d, row_bytes);
 #pragma unroll
         for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
       }
@@ -178,7 +182,11 @@ k_fwd(const typename T::storage* __restrict__ v, const typename T::storage* __re
   }
 
   if (!live) return;
-  const float inv_l = 1.0f / l_run;
+  if (m_out != nullptr && seg == 0 && lane == 0) {
+    m_out[tok] = m_run;
+    l_out[tok] = l_run;
+  }
+  const float inv_l = normalize ? 1.0f / l_run : 1.0f;
   const auto orr = make_rsrc(out + tok * d, row_bytes);
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
@@ -194,8 +202,7 @@ k_fwd(const typename T::storage* __restrict__ v, const typename T::storage* __re
 // Same bytes, geometry and launch shape as k_fwd, no softmax: out = sum_n v_n.
 template <class T, int W, int VPL, int NR>
 __global__ void __launch_bounds__(FwdGeom<W>::kBlock)
-k_sol(const typename T::storage* __restrict__ v, typename T::storage* __restrict__ out, int n_src,
-      int64_t n_tok, int d, int64_t src_stride) {
+k_sol(const RowTable v, typename T::storage* __restrict__ out, int n_src, int64_t n_tok, int d) {
   using S = typename T::storage;
   constexpr int CE = T::ce;
   constexpr int TPB = FwdGeom<W>::kTpb;
@@ -218,7 +225,7 @@ k_sol(const typename T::storage* __restrict__ v, typename T::storage* __restrict
 #pragma unroll
     for (int n = 0; n < NR; ++n) {
       if (n < rows) {
-        const auto r = make_rsrc(v + (int64_t)(c0 + n) * src_stride + tok * d, row_bytes);
+        const auto r = make_rsrc(row_of<const S>(v, c0 + n) + tok * d, row_bytes);
 #pragma unroll
         for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
       }
@@ -243,9 +250,10 @@ k_sol(const typename T::storage* __restrict__ v, typename T::storage* __restrict
 // a softmax and a weighted sum. v is read once for all S outputs.
 template <class T, int W, int VPL, int NR>
 __global__ void __launch_bounds__(FwdGeom<W>::kBlock)
-k_batched(const typename T::storage* __restrict__ v, const typename T::storage* __restrict__ q,
-          typename T::storage* __restrict__ out, int n_src, int n_q, int64_t n_tok, int d,
-          int64_t src_stride, float eps, float inv_d) {
+k_batched(const RowTable v, const typename T::storage* __restrict__ q,
+          typename T::storage* __restrict__ out, float* __restrict__ m_out,
+          float* __restrict__ l_out, int normalize, int n_src, int n_q, int64_t n_tok, int d,
+          float eps, float inv_d) {
   using S = typename T::storage;
   constexpr int CE = T::ce;
   constexpr int TPB = FwdGeom<W>::kTpb;
@@ -270,7 +278,7 @@ k_batched(const typename T::storage* __restrict__ v, const typename T::storage* 
 #pragma unroll
   for (int n = 0; n < NR; ++n) {
     if (n < rows) {
-      const auto r = make_rsrc(v + (int64_t)n * src_stride + tok * d, row_bytes);
+      const auto r = make_rsrc(row_of<const S>(v, n) + tok * d, row_bytes);
 #pragma unroll
       for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
     }
@@ -332,7 +340,11 @@ k_batched(const typename T::storage* __restrict__ v, const typename T::storage* 
       }
     }
     if (live) {
-      const float inv_l = 1.0f / l;
+      if (m_out != nullptr && seg == 0 && lane == 0) {
+        m_out[(int64_t)s * n_tok + tok] = m;
+        l_out[(int64_t)s * n_tok + tok] = l;
+      }
+      const float inv_l = normalize ? 1.0f / l : 1.0f;
       const auto orr = make_rsrc(out + ((int64_t)s * n_tok + tok) * d, row_bytes);
 #pragma unroll
       for (int j = 0; j < VPL; ++j) {
@@ -358,9 +370,10 @@ k_batched(const typename T::storage* __restrict__ v, const typename T::storage* 
 // every wave of the workgroup meets the same barriers.
 template <class T, int W, int VPL, int NR>
 __global__ void __launch_bounds__(FwdGeom<W>::kBlock)
-k_fwd_res(const typename T::storage* __restrict__ v, const typename T::storage* __restrict__ w,
-          typename T::storage* __restrict__ out, float* __restrict__ stats, int n_src,
-          int64_t n_tok, int d, int64_t src_stride, float eps, float inv_d, int n_iter) {
+k_fwd_res(const RowTable v, const typename T::storage* __restrict__ w,
+          typename T::storage* __restrict__ out, float* __restrict__ stats,
+          float* __restrict__ m_out, float* __restrict__ l_out, int normalize, int n_src,
+          int64_t n_tok, int d, float eps, float inv_d, int n_iter) {
   using S = typename T::storage;
   constexpr int CE = T::ce;
   constexpr int TPB = FwdGeom<W>::kTpb;
@@ -395,7 +408,7 @@ k_fwd_res(const typename T::storage* __restrict__ v, const typename T::storage* 
 #pragma unroll
     for (int n = 0; n < NR; ++n) {
       if (n < rows) {
-        const auto r = make_rsrc(v + (int64_t)n * src_stride + t0 * d, row_bytes);
+        const auto r = make_rsrc(row_of<const S>(v, n) + t0 * d, row_bytes);
 #pragma unroll
         for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
       }
@@ -451,7 +464,7 @@ k_fwd_res(const typename T::storage* __restrict__ v, const typename T::storage* 
 #pragma unroll
           for (int e = 0; e < CE; ++e) acc[j][e] = fmaf(p, elem<T>(x[n][j], e), acc[j][e]);
         if (more) {
-          const auto r = make_rsrc(v + (int64_t)n * src_stride + nxt * d, row_bytes);
+          const auto r = make_rsrc(row_of<const S>(v, n) + nxt * d, row_bytes);
 #pragma unroll
           for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
         }
@@ -467,7 +480,11 @@ k_fwd_res(const typename T::storage* __restrict__ v, const typename T::storage* 
           }
         }
       }
-      const float inv_l = 1.0f / l;
+      if (m_out != nullptr && seg == 0 && lane == 0) {
+        m_out[tok] = m;
+        l_out[tok] = l;
+      }
+      const float inv_l = normalize ? 1.0f / l : 1.0f;
       const auto orr = make_rsrc(out + tok * d, row_bytes);
 #pragma unroll
       for (int j = 0; j < VPL; ++j) {
@@ -486,8 +503,8 @@ k_fwd_res(const typename T::storage* __restrict__ v, const typename T::storage* 
 // softmax (out = sum_n v_n).
 template <class T, int W, int VPL, int NR>
 __global__ void __launch_bounds__(FwdGeom<W>::kBlock)
-k_sol_res(const typename T::storage* __restrict__ v, typename T::storage* __restrict__ out,
-          int n_src, int64_t n_tok, int d, int64_t src_stride) {
+k_sol_res(const RowTable v, typename T::storage* __restrict__ out, int n_src, int64_t n_tok,
+          int d) {
   using S = typename T::storage;
   constexpr int CE = T::ce;
   constexpr int TPB = FwdGeom<W>::kTpb;
@@ -506,7 +523,7 @@ k_sol_res(const typename T::storage* __restrict__ v, typename T::storage* __rest
 #pragma unroll
   for (int n = 0; n < NR; ++n) {
     if (n < rows) {
-      const auto r = make_rsrc(v + (int64_t)n * src_stride + first * d, row_bytes);
+      const auto r = make_rsrc(row_of<const S>(v, n) + first * d, row_bytes);
 #pragma unroll
       for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
     }
@@ -527,7 +544,7 @@ k_sol_res(const typename T::storage* __restrict__ v, typename T::storage* __rest
 #pragma unroll
           for (int e = 0; e < CE; ++e) acc[j][e] += elem<T>(x[n][j], e);
         if (more) {
-          const auto r = make_rsrc(v + (int64_t)n * src_stride + (tok + slots) * d, row_bytes);
+          const auto r = make_rsrc(row_of<const S>(v, n) + (tok + slots) * d, row_bytes);
 #pragma unroll
           for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
         }
@@ -552,6 +569,12 @@ k_sol_res(const typename T::storage* __restrict__ v, typename T::storage* __rest
 //     dw      += sum_n da_n v_n
 // STATS: logit_n and r_n come from the forward's stats, so only G_n is reduced
 // over D; otherwise a_n and ssq_n are recomputed as in the forward.
+// gm != nullptr selects the gradient of the unnormalised triple (o, m, l) of
+// attn_with_stats instead: g is dL/do, gm/gl are dL/dm and dL/dl per token.
+// With p_n = exp(logit_n - m) and k the (first) row holding the max logit,
+//     dlogit_n = p_n (G_n + gl)                              n != k
+//     dlogit_k = gm - sum_{n != k} p_n (G_n + gl)           (p_k = 1, m = logit_k)
+// and dv_n = p_n g + da_n w + c_n v_n with da_n, c_n as above.
 // grad_out and each source row are refilled with the next token's data as soon
 // as they have been consumed.
 // dw: each slot accumulates in registers; at the end the slots are folded in
@@ -559,10 +582,11 @@ k_sol_res(const typename T::storage* __restrict__ v, typename T::storage* __rest
 // No float atomics anywhere, so dw is bit-reproducible for a given grid.
 template <class T, int W, int VPL, int NR, bool STATS>
 __global__ void __launch_bounds__(BwdGeom<W>::kBlock)
-k_bwd(const typename T::storage* __restrict__ v, const typename T::storage* __restrict__ w,
+k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
       const typename T::storage* __restrict__ g, const float* __restrict__ stats,
-      typename T::storage* __restrict__ dv, float* __restrict__ partial, int n_src, int64_t n_tok,
-      int d, int64_t src_stride, float eps, float inv_d, int n_iter) {
+      const float* __restrict__ gm, const float* __restrict__ gl, const RowTable dv,
+      float* __restrict__ partial, int n_src, int64_t n_tok, int d, float eps, float inv_d,
+      int n_iter) {
   using S = typename T::storage;
   constexpr int CE = T::ce;
   constexpr int TPB = BwdGeom<W>::kTpb;
@@ -585,7 +609,6 @@ k_bwd(const typename T::storage* __restrict__ v, const typename T::storage* __re
   const uint32_t lane_off = (uint32_t)(seg * 64 + lane) * 16u;
   const int64_t slots = (int64_t)gridDim.x * TPB;
   const int64_t first = (int64_t)blockIdx.x * TPB + slot;
-  const int64_t dv_stride = n_tok * d;
   const int rows = n_src;  // host guarantees n_src <= NR
   int iters = n_iter;
   if constexpr (W == 1) {
@@ -617,7 +640,7 @@ k_bwd(const typename T::storage* __restrict__ v, const typename T::storage* __re
 #pragma unroll
     for (int n = 0; n < NR; ++n) {
       if (n < rows) {
-        const auto r = make_rsrc(v + (int64_t)n * src_stride + t0 * d, row_bytes);
+        const auto r = make_rsrc(row_of<const S>(v, n) + t0 * d, row_bytes);
 #pragma unroll
         for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
       }
@@ -665,6 +688,7 @@ k_bwd(const typename T::storage* __restrict__ v, const typename T::storage* __re
     // its tiny dlogit to full relative precision instead of G_max - S ~ 0.
     float lg[NR], rr[NR];
     float m = -INFINITY, gref = 0.0f;
+    int top = 0;
 #pragma unroll
     for (int n = 0; n < NR; ++n) {
       if (n < rows) {
@@ -678,6 +702,7 @@ k_bwd(const typename T::storage* __restrict__ v, const typename T::storage* __re
         if (lg[n] > m) {
           m = lg[n];
           gref = part[n];
+          top = n;
         }
       }
     }
@@ -689,15 +714,30 @@ k_bwd(const typename T::storage* __restrict__ v, const typename T::storage* __re
         al[n] = expf(lg[n] - m);
         l += al[n];
       }
-    const float inv_l = 1.0f / l;
+    // Afterwards dlogit_n = al[n] * (part[n] - sdev) in both modes.
     float sdev = 0.0f;
+    if (gm == nullptr) {
+      const float inv_l = 1.0f / l;
 #pragma unroll
-    for (int n = 0; n < NR; ++n)
-      if (n < rows) {
-        al[n] *= inv_l;
-        part[n] -= gref;
-        sdev = fmaf(al[n], part[n], sdev);
-      }
+      for (int n = 0; n < NR; ++n)
+        if (n < rows) {
+          al[n] *= inv_l;
+          part[n] -= gref;
+          sdev = fmaf(al[n], part[n], sdev);
+        }
+    } else {
+      const float glv = gl[tok], gmv = gm[tok];
+      float other = 0.0f;
+#pragma unroll
+      for (int n = 0; n < NR; ++n)
+        if (n < rows) {
+          part[n] += glv;
+          if (n != top) other = fmaf(al[n], part[n], other);
+        }
+#pragma unroll
+      for (int n = 0; n < NR; ++n)
+        if (n < rows && n == top) part[n] = gmv - other;
+    }
 
     float gf[VPL][CE];
 #pragma unroll
@@ -717,7 +757,7 @@ k_bwd(const typename T::storage* __restrict__ v, const typename T::storage* __re
         const float da = dlogit * rr[n];
         const float c = -dlogit * lg[n] * rr[n] * rr[n] * inv_d;
         const float da_w = da * dw_on;
-        const auto dr = make_rsrc(dv + (int64_t)n * dv_stride + tok * d, live ? row_bytes : 0u);
+        const auto dr = make_rsrc(row_of<S>(dv, n) + tok * d, live ? row_bytes : 0u);
 #pragma unroll
         for (int j = 0; j < VPL; ++j) {
           float f[CE];
@@ -730,7 +770,7 @@ k_bwd(const typename T::storage* __restrict__ v, const typename T::storage* __re
           st16_stream(dr, lane_off + j * kStep, pack<T>(f));
         }
         if (more) {
-          const auto r = make_rsrc(v + (int64_t)n * src_stride + nxt * d, row_bytes);
+          const auto r = make_rsrc(row_of<const S>(v, n) + nxt * d, row_bytes);
 #pragma unroll
           for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
         }
@@ -768,6 +808,220 @@ k_bwd(const typename T::storage* __restrict__ v, const typename T::storage* __re
 #pragma unroll
         for (int e = 0; e < 4; ++e) t[e] = __float_as_int(dwa[j][q4 * 4 + e]);
         st16(pr, base + q4 * 16u, t);
+      }
+    }
+  }
+}
+
+
+// ------------------------------------------------------- batched backward
+//
+// Gradient of the batched forward out[s] = AttnRes(v, q_s), s < n_q <= SQ, for
+// grad_out g [S][n_tok][D]. The S queries are S operators sharing v, so per
+// token (with alpha, logit, r of query s, G_sn = <g_s, v_n>):
+//     dlogit_sn = alpha_sn (G_sn - sum_k alpha_sk G_sk)   [relative to the top row]
+//     da_sn     = dlogit_sn r_n,   c_n = -sum_s dlogit_sn logit_sn r_n^2 / D
+//     dv_n      = sum_s (alpha_sn g_s + da_sn q_s) + c_n v_n
+//     dq_s     += sum_n da_sn v_n
+// The token's N rows are read once for all queries; dv is accumulated over the
+// queries in fp32 registers and rounded once; dq_s is accumulated over the
+// workgroup's tokens in LDS (each lane owns its float4 slots, so no barrier
+// is needed until the end) and written as one fp32 partial row per query
+// ([grid][n_q][D]), reduced afterwards in a fixed order like dw. Registers
+// would hold dv's NR x CE and the tile, but not SQ x CE more without spilling.
+// One token per W waves with one chunk per lane (VPL = 1), persistent and
+// pipelined like k_bwd. Reference: the batched forward is
+// src/switchyard/triton_op.py:378-501; it has no backward.
+template <class T, int W, int NR, int SQ>
+__global__ void __launch_bounds__(FwdGeom<W>::kBlock)
+k_bwd_batched(const RowTable v, const typename T::storage* __restrict__ q,
+              const typename T::storage* __restrict__ g, const RowTable dv,
+              float* __restrict__ partial, int n_src, int n_q, int64_t n_tok, int d, float eps,
+              float inv_d, int n_iter) {
+  using S = typename T::storage;
+  constexpr int CE = T::ce;
+  constexpr int TPB = FwdGeom<W>::kTpb;
+  constexpr int kQ4 = SQ * CE / 4;  // float4 dq accumulators per lane
+  // Two ping-pong buffer pairs: red1 for the sums of squares (once per
+  // token), red for the per-query dots (`phase` advances per exchange).
+  __shared__ float red1[2][TPB][W][NR];
+  __shared__ float red[2][TPB][W][2 * NR];
+  // dq accumulators, lane-contiguous float4: dql[wave][s*CE/4 + c][lane].
+  __shared__ float4 dql[TPB * W][kQ4][64];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int slot = wave / W;
+  const int seg = wave % W;
+  const uint32_t row_bytes = (uint32_t)d * sizeof(S);
+  const uint32_t lane_off = (uint32_t)(seg * 64 + lane) * 16u;
+  const int64_t slots = (int64_t)gridDim.x * TPB;
+  const int64_t first = (int64_t)blockIdx.x * TPB + slot;
+  const int rows = n_src;  // host guarantees n_src <= NR and n_q <= SQ
+  int iters = n_iter;
+  if constexpr (W == 1) iters = first < n_tok ? (int)((n_tok - first + slots - 1) / slots) : 0;
+
+#pragma unroll
+  for (int c = 0; c < kQ4; ++c) dql[wave][c][lane] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+
+  i32x4_t x[NR];
+  {
+    const int64_t t0 = first < n_tok ? first : n_tok - 1;
+#pragma unroll
+    for (int n = 0; n < NR; ++n)
+      if (n < rows) x[n] = ld16_stream(make_rsrc(row_of<const S>(v, n) + t0 * d, row_bytes), lane_off);
+  }
+
+  [[maybe_unused]] int phase = 0;
+  for (int k = 0; k < iters; ++k) {
+    const int64_t tok_raw = first + (int64_t)k * slots;
+    const bool live = tok_raw < n_tok;
+    const int64_t tok = live ? tok_raw : n_tok - 1;
+    const bool more = k + 1 < iters;
+    const int64_t nxt = tok_raw + slots < n_tok ? tok_raw + slots : n_tok - 1;
+
+    float rr[NR];
+#pragma unroll
+    for (int n = 0; n < NR; ++n)
+      if (n < rows) rr[n] = wave_sum(dot<T>(x[n], x[n], 0.0f));
+    if constexpr (W > 1) cross_wave_sum<W, 1, NR, TPB>(rr, 1, rows, red1[k & 1], slot, seg, lane);
+#pragma unroll
+    for (int n = 0; n < NR; ++n)
+      if (n < rows) rr[n] = rsqrtf(fmaf(rr[n], inv_d, eps));
+
+    float dva[NR][CE];
+    float cacc[NR];
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      cacc[n] = 0.0f;
+#pragma unroll
+      for (int e = 0; e < CE; ++e) dva[n][e] = 0.0f;
+    }
+
+    // Queries in a runtime loop; query s+1's rows are loaded while s is used.
+    i32x4_t gq = ld16_stream(make_rsrc(g + tok * d, row_bytes), lane_off);
+    i32x4_t qq = ld16(make_rsrc(q, row_bytes), lane_off);
+#pragma unroll 1
+    for (int s = 0; s < n_q; ++s) {
+      // Keep the tile opaque to loop-invariant motion: otherwise its fp32
+      // conversions are hoisted out of the query loop (NR x CE more VGPRs).
+#pragma unroll
+      for (int n = 0; n < NR; ++n)
+        if (n < rows) asm volatile("" : "+v"(x[n]));
+      {
+        i32x4_t gn = gq, qn = qq;
+        if (s + 1 < n_q) {
+          gn = ld16_stream(make_rsrc(g + ((int64_t)(s + 1) * n_tok + tok) * d, row_bytes), lane_off);
+          qn = ld16(make_rsrc(q + (int64_t)(s + 1) * d, row_bytes), lane_off);
+        }
+        float part[2 * NR];
+#pragma unroll
+        for (int n = 0; n < NR; ++n) {
+          if (n < rows) {
+            part[n] = wave_sum(dot<T>(x[n], gq, 0.0f));
+            part[NR + n] = wave_sum(dot<T>(x[n], qq, 0.0f));
+          }
+        }
+        if constexpr (W > 1) cross_wave_sum<W, 2, NR, TPB>(part, 2, rows, red[phase++ & 1], slot, seg, lane);
+        float lg[NR], al[NR];
+        float m = -INFINITY, gref = 0.0f;
+#pragma unroll
+        for (int n = 0; n < NR; ++n) {
+          if (n < rows) {
+            lg[n] = part[NR + n] * rr[n];
+            if (lg[n] > m) {
+              m = lg[n];
+              gref = part[n];
+            }
+          }
+        }
+        float l = 0.0f;
+#pragma unroll
+        for (int n = 0; n < NR; ++n)
+          if (n < rows) {
+            al[n] = expf(lg[n] - m);
+            l += al[n];
+          }
+        const float inv_l = 1.0f / l;
+        float sdev = 0.0f;
+#pragma unroll
+        for (int n = 0; n < NR; ++n)
+          if (n < rows) {
+            al[n] *= inv_l;
+            part[n] -= gref;
+            sdev = fmaf(al[n], part[n], sdev);
+          }
+        float u[CE];
+#pragma unroll
+        for (int e = 0; e < CE; ++e) u[e] = 0.0f;
+#pragma unroll
+        for (int n = 0; n < NR; ++n) {
+          if (n < rows) {
+            const float dlogit = al[n] * (part[n] - sdev);
+            const float da = dlogit * rr[n];
+            cacc[n] = fmaf(-dlogit * lg[n], rr[n] * rr[n] * inv_d, cacc[n]);
+#pragma unroll
+            for (int e = 0; e < CE; ++e) {
+              dva[n][e] = fmaf(al[n], elem<T>(gq, e), fmaf(da, elem<T>(qq, e), dva[n][e]));
+              u[e] = fmaf(da, elem<T>(x[n], e), u[e]);
+            }
+          }
+        }
+        if (live) {
+#pragma unroll
+          for (int c = 0; c < CE / 4; ++c) {
+            float4 a = dql[wave][s * (CE / 4) + c][lane];
+            a.x += u[4 * c];
+            a.y += u[4 * c + 1];
+            a.z += u[4 * c + 2];
+            a.w += u[4 * c + 3];
+            dql[wave][s * (CE / 4) + c][lane] = a;
+          }
+        }
+        gq = gn;
+        qq = qn;
+      }
+    }
+
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      if (n < rows) {
+        float f[CE];
+#pragma unroll
+        for (int e = 0; e < CE; ++e) f[e] = fmaf(cacc[n], elem<T>(x[n], e), dva[n][e]);
+        st16_stream(make_rsrc(row_of<S>(dv, n) + tok * d, live ? row_bytes : 0u), lane_off, pack<T>(f));
+        if (more) x[n] = ld16_stream(make_rsrc(row_of<const S>(v, n) + nxt * d, row_bytes), lane_off);
+      }
+    }
+  }
+
+  // Sum the TPB slots' accumulators in slot order, then one fp32 partial row
+  // per query: partial[blockIdx][s][:].
+  __syncthreads();
+  if (slot == 0) {
+    const uint32_t base = (lane_off / 16u) * CE * 4u;
+#pragma unroll
+    for (int s = 0; s < SQ; ++s) {
+      if (s < n_q) {
+        const auto pr = make_rsrc(partial + ((int64_t)blockIdx.x * n_q + s) * d, (uint32_t)d * 4u);
+#pragma unroll
+        for (int c = 0; c < CE / 4; ++c) {
+          float4 a = dql[seg][s * (CE / 4) + c][lane];
+#pragma unroll
+          for (int k = 1; k < TPB; ++k) {
+            const float4 b = dql[k * W + seg][s * (CE / 4) + c][lane];
+            a.x += b.x;
+            a.y += b.y;
+            a.z += b.z;
+            a.w += b.w;
+          }
+          i32x4_t t;
+          t[0] = __float_as_int(a.x);
+          t[1] = __float_as_int(a.y);
+          t[2] = __float_as_int(a.z);
+          t[3] = __float_as_int(a.w);
+          st16(pr, base + c * 16u, t);
+        }
       }
     }
   }

@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include "../../include/switchyard.h"
+#include "sy_device.hpp"
 
 namespace sy {
 
@@ -22,47 +23,78 @@ namespace sy {
 constexpr int64_t kGenericMaxN = 4096;
 // Largest query count of the resident batched kernel.
 constexpr int64_t kBatchedMaxQ = 16;
+// Register-resident batched backward: at most this many sources and queries.
+constexpr int64_t kBwdBatchedMaxN = 9;
+constexpr int64_t kBwdBatchedMaxQ = 8;
+// Dynamic LDS the generic kernels may request (bytes).
+constexpr int64_t kGenericMaxLds = 64 * 1024;
+// LDS of the generic batched backward: per-(query, row) alpha and da, per-row
+// c and r, the row-scalar scratch and the block-reduction scratch.
+inline int64_t bwd_batched_generic_lds(int64_t n_src, int64_t n_q) {
+  return (2 * n_q * n_src + 5 * n_src + 257) * (int64_t)sizeof(float);
+}
 
+// Source rows are addressed through a RowTable (sy_device.hpp) in every
+// launch: the stacked layout and a per-source pointer list look the same to
+// the kernels.
 struct FwdArgs {
-  const void* v;
+  RowTable v;
   const void* w;
   void* out;
-  float* stats;
+  float* stats;   // [2][N][n_tok] logits and r, or nullptr
+  float* m_out;   // [n_tok] max logit, or nullptr (then l_out is nullptr too)
+  float* l_out;   // [n_tok] sum of exp(logit - m)
+  int normalize;  // 1: out = o / l (the operator); 0: out = o (attn_with_stats)
   int n_src;
   int64_t n_tok;
   int d;
-  int64_t src_stride;
   int v_dtype;
   int w_dtype;
   float eps;
 };
 
 struct BwdArgs {
-  const void* v;
+  RowTable v;
   const void* w;
   const void* g;
   const float* stats;
-  void* dv;
-  void* dw;
-  float* partial;  // [grid][d] fp32
+  const float* gm;  // dL/dm [n_tok] for the (o, m, l) gradient, or nullptr
+  const float* gl;  // dL/dl [n_tok]
+  RowTable dv;
+  float* partial;   // [grid][d] fp32
   int n_src;
   int64_t n_tok;
   int d;
-  int64_t src_stride;
   int v_dtype;
   int w_dtype;
   float eps;
 };
 
 struct BatchedArgs {
-  const void* v;
+  RowTable v;
   const void* q;
   void* out;
+  float* m_out;  // [S][n_tok] or nullptr
+  float* l_out;  // [S][n_tok]
+  int normalize;
   int n_src;
   int n_q;
   int64_t n_tok;
   int d;
-  int64_t src_stride;
+  int dtype;
+  float eps;
+};
+
+struct BwdBatchedArgs {
+  RowTable v;
+  const void* q;     // [S][d]
+  const void* g;     // [S][n_tok][d]
+  RowTable dv;
+  float* partial;    // [grid][S][d] fp32
+  int n_src;
+  int n_q;
+  int64_t n_tok;
+  int d;
   int dtype;
   float eps;
 };
@@ -96,16 +128,57 @@ struct KernelRes {
   hipError_t launch_sol_vec_##NAME(const sy_plan& p, const FwdArgs& a, hipStream_t s);         \
   hipError_t launch_batched_vec_##NAME(const sy_plan& p, const BatchedArgs& a, hipStream_t s); \
   hipError_t launch_bwd_vec_##NAME(const sy_plan& p, const BwdArgs& a, int grid, hipStream_t s); \
-  hipError_t bwd_vec_resources_##NAME(const sy_plan& p, bool stats, KernelRes* out);
+  hipError_t bwd_vec_resources_##NAME(const sy_plan& p, bool stats, KernelRes* out);          \
+  hipError_t launch_bwd_batched_vec_##NAME(const sy_plan& p, const BwdBatchedArgs& a, int grid, \
+                                           hipStream_t s);                                    \
+  hipError_t bwd_batched_vec_resources_##NAME(const sy_plan& p, KernelRes* out);
 SY_DECLARE_VEC(bf16)
 SY_DECLARE_VEC(f16)
 SY_DECLARE_VEC(f32)
 #undef SY_DECLARE_VEC
 
+// Merge of two (o, m, l) partial results and its gradient (sy_merge.hip).
+// `vec` selects the 16-byte path (every row start 16-byte aligned).
+struct MergeArgs {
+  const void* o1;
+  const float* m1;
+  const float* l1;
+  const void* o2;
+  const float* m2;
+  const float* l2;
+  void* o;
+  float* m;
+  float* l;
+  int64_t n_tok;
+  int d;
+};
+struct MergeBwdArgs {
+  const void* o1;
+  const float* m1;
+  const float* l1;
+  const void* o2;
+  const float* m2;
+  const float* l2;
+  const void* go;
+  const float* gm;
+  const float* gl;
+  void* do1;
+  float* dm1;
+  float* dl1;
+  void* do2;
+  float* dm2;
+  float* dl2;
+  int64_t n_tok;
+  int d;
+};
+hipError_t launch_merge(const MergeArgs& a, int dtype, bool vec, hipStream_t s);
+hipError_t launch_merge_bwd(const MergeBwdArgs& a, int dtype, bool vec, hipStream_t s);
+
 // Generic kernels, the dw reduction and the probes (sy_generic.hip).
 hipError_t launch_fwd_generic(const FwdArgs& a, hipStream_t s);
 hipError_t launch_sol_generic(const FwdArgs& a, hipStream_t s);
 hipError_t launch_bwd_generic(const BwdArgs& a, int grid, hipStream_t s);
+hipError_t launch_bwd_batched_generic(const BwdBatchedArgs& a, int grid, hipStream_t s);
 hipError_t launch_dw_reduce(const float* partial, int rows, int d, void* dw, int w_dtype,
                             hipStream_t s);
 hipError_t launch_probe(int kind, const void* src, void* dst, int64_t bytes, int grid,

@@ -14,6 +14,9 @@
 //  4. Backward with no resident fit under its budget: generic (a fatter tile
 //     would spill: the backward runs two waves per SIMD at most 256 VGPRs).
 //  5. Batched: resident with S <= 16, else one forward launch per query.
+//  6. Batched backward: one chunk per lane on the fewest waves that cover the
+//     row, N <= 9 and S <= 8 (dv and dq accumulators stay in registers);
+//     otherwise the generic kernel while its LDS scalars fit.
 #include <cstdio>
 #include <cstdlib>
 
@@ -85,16 +88,30 @@ bool resident(int64_t n_src, int64_t e, int budget, int max_vpl, int* w_out, int
 int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_dtype,
               int aligned, sy_plan* out) {
   if (out == nullptr) return SY_ERR_NULL;
-  if (op < SY_OP_FWD || op > SY_OP_SOL) return SY_ERR_OP;
+  if (op < SY_OP_FWD || op > SY_OP_BWD_BATCHED) return SY_ERR_OP;
   if (!valid_dtype(v_dtype) || !valid_dtype(w_dtype)) return SY_ERR_DTYPE;
-  if (n_src < 1 || d < 1 || (op == SY_OP_BATCHED && n_q < 1)) return SY_ERR_SHAPE;
-  if (n_src > 0x7fffffff || d > 0x7fffffff / 16) return SY_ERR_SHAPE;
+  const bool batched = op == SY_OP_BATCHED || op == SY_OP_BWD_BATCHED;
+  if (n_src < 1 || d < 1 || (batched && n_q < 1)) return SY_ERR_SHAPE;
+  if (n_src > 0x7fffffff || d > 0x7fffffff / 16 || n_q > 0x7fffffff) return SY_ERR_SHAPE;
 
   const int ce = v_dtype == SY_F32 ? 4 : 8;
-  const bool same_w = op == SY_OP_SOL || op == SY_OP_BATCHED || v_dtype == w_dtype;
+  const bool same_w = op == SY_OP_SOL || batched || v_dtype == w_dtype;
   const bool vec = aligned && (d % ce == 0) && same_w;
   const int64_t e = d / ce;
   int w = 0, vpl = 0, nr = 0;
+
+  if (op == SY_OP_BWD_BATCHED) {
+    if (vec && n_src <= kBwdBatchedMaxN && n_q <= kBwdBatchedMaxQ) {
+      for (int ww : kWaves) {
+        if ((int64_t)64 * ww < e) continue;
+        set(out, SY_FAMILY_RESIDENT, ww, 1, n_src <= 4 ? 4 : 9, ce, op, n_src);
+        return SY_OK;
+      }
+    }
+    if (bwd_batched_generic_lds(n_src, n_q) > kGenericMaxLds) return SY_ERR_SHAPE;
+    set(out, SY_FAMILY_GENERIC, 4, 0, 0, 1, op, n_src);
+    return SY_OK;
+  }
 
   if (vec && !(op == SY_OP_BATCHED && n_q > kBatchedMaxQ)) {
     const int budget =

@@ -18,7 +18,7 @@ import torch  # noqa: F401  -- must precede the load: provides the HIP runtime
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "libswitchyard_hip.so"
 
 SY_F32, SY_F16, SY_BF16 = 0, 1, 2
-OP_FWD, OP_BWD, OP_BATCHED, OP_SOL = 0, 1, 2, 3
+OP_FWD, OP_BWD, OP_BATCHED, OP_SOL, OP_BWD_BATCHED = 0, 1, 2, 3, 4
 FAMILY_NAMES = {0: "resident", 1: "chunked", 2: "generic", 3: "per_query"}
 
 _DTYPE_CODES = {torch.float32: SY_F32, torch.float16: SY_F16, torch.bfloat16: SY_BF16}
@@ -26,6 +26,10 @@ _DTYPE_CODES = {torch.float32: SY_F32, torch.float16: SY_F16, torch.bfloat16: SY
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int
+_vpp = ctypes.POINTER(ctypes.c_void_p)  # host array of device pointers
+
+#: Largest source count of the pointer-table entry points (SY_MAX_TABLE_ROWS).
+MAX_TABLE_ROWS = 16
 
 
 class Plan(ctypes.Structure):
@@ -63,6 +67,22 @@ SIGNATURES = {
     "sy_dw_reduce": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp]),
     "sy_fwd_batched": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32, ctypes.c_float, _vp]),
     "sy_sol": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp]),
+    "sy_fwd_table": (_i32, [_vpp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, ctypes.c_float, _vp]),
+    "sy_bwd_table": (_i32, [_vpp, _vp, _vp, _vp, _vpp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32,
+                            ctypes.c_float, _vp]),
+    "sy_fwd_batched_table": (_i32, [_vpp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, ctypes.c_float,
+                                    _vp]),
+    "sy_attn_with_stats": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32,
+                                  ctypes.c_float, _vp]),
+    "sy_attn_with_stats_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
+                                      _i64, _i64, _i32, _i32, ctypes.c_float, _vp]),
+    "sy_batched_with_stats": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32,
+                                     ctypes.c_float, _vp]),
+    "sy_merge_stats": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp]),
+    "sy_merge_stats_bwd": (_i32, [_vp] * 15 + [_i64, _i64, _i32, _vp]),
+    "sy_bwd_batched_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i32]),
+    "sy_bwd_batched": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i32,
+                              ctypes.c_float, _vp]),
     "sy_bw_probe": (_i32, [_i32, _vp, _vp, _i64, _vp]),
     "sy_probe_grid": (_i64, [_i64]),
     "sy_strerror": (ctypes.c_char_p, [_i32]),
@@ -118,6 +138,11 @@ def plan(op: int, n_src: int, d: int, dtype: torch.dtype, *, n_q: int = 0,
                            int(aligned), ctypes.byref(p))
     check(rc, "sy_plan_for")
     return p.as_dict()
+
+
+def pointer_table(tensors) -> ctypes.Array:
+    """A host array of the tensors' device addresses, for the *_table entry points."""
+    return (ctypes.c_void_p * len(tensors))(*[t.data_ptr() for t in tensors])
 
 
 def stream_ptr(device: torch.device) -> ctypes.c_void_p:

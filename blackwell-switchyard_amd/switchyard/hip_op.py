@@ -34,6 +34,7 @@ from .reference import DEFAULT_EPS
 __all__ = [
     "block_attn_res_hip",
     "block_attn_res_batched",
+    "block_attn_res_batched_train",
     "BlockAttnResHIP",
     "speed_of_light",
     "bandwidth_probe",
@@ -134,17 +135,8 @@ def block_attn_res_hip(v: torch.Tensor, w: torch.Tensor, eps: float = DEFAULT_EP
     return _BlockAttnResHIP.apply(v, w, eps)
 
 
-def block_attn_res_batched(
-    v: torch.Tensor, queries: torch.Tensor, eps: float = DEFAULT_EPS
-) -> torch.Tensor:
-    """``S`` pseudo-queries against one shared read of ``v`` (output only).
-
-    Same contract as the reference's ``block_attn_res_batched``
-    (triton_op.py:438-501): ``out[s] == block_attn_res_triton(v, queries[s])``,
-    ``[S, B, T, D]``, no backward. For N, D, dtype the resident kernel holds
-    and S <= 16 one kernel reads ``v`` once; other shapes issue one forward
-    launch per query, written straight into ``out[s]`` (no stack).
-    """
+def _validate_batched(v: torch.Tensor, queries: torch.Tensor) -> None:
+    """The reference's batched checks and messages (triton_op.py:438-462)."""
     if v.ndim != 4:
         raise ValueError(f"v must be [N, B, T, D], got {tuple(v.shape)}")
     if queries.ndim != 2 or queries.shape[1] != v.shape[-1]:
@@ -157,27 +149,93 @@ def block_attn_res_batched(
         raise ValueError("v and queries must have the same dtype")
     if v.shape[0] == 0 or queries.shape[0] == 0 or v.shape[-1] == 0:
         raise ValueError("N, S, and D must be positive")
-    if v.requires_grad or queries.requires_grad:
-        raise RuntimeError(
-            "block_attn_res_batched has no backward; use block_attn_res_triton per query "
-            "for training, or run this under torch.no_grad() for inference"
-        )
-    dt = _lib.dtype_code(v.dtype)
+    _lib.dtype_code(v.dtype)
+
+
+def _batched_forward(v: torch.Tensor, queries: torch.Tensor, eps: float) -> torch.Tensor:
     n, b, t, d = v.shape
     s = queries.shape[0]
-    v = v.contiguous()
-    queries = queries.contiguous()
     out = torch.empty(s, b, t, d, device=v.device, dtype=v.dtype)
     n_tok = b * t
     if n_tok == 0:
         return out
     with torch.cuda.device(v.device):
         rc = _lib.lib().sy_fwd_batched(
-            _ptr(v), _ptr(queries), _ptr(out), n, s, n_tok, d, n_tok * d, dt, float(eps),
-            _lib.stream_ptr(v.device),
+            _ptr(v), _ptr(queries), _ptr(out), n, s, n_tok, d, n_tok * d,
+            _lib.dtype_code(v.dtype), float(eps), _lib.stream_ptr(v.device),
         )
     _lib.check(rc, "sy_fwd_batched")
     return out
+
+
+class _BlockAttnResBatched(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, v: torch.Tensor, queries: torch.Tensor, eps: float):
+        _validate_batched(v, queries)
+        v = v.contiguous()
+        queries = queries.contiguous()
+        ctx.save_for_backward(v, queries)
+        ctx.eps = float(eps)
+        return _batched_forward(v, queries, eps)
+
+    @staticmethod
+    def backward(ctx, grad_out: torch.Tensor):
+        v, queries = ctx.saved_tensors
+        n, b, t, d = v.shape
+        s = queries.shape[0]
+        n_tok = b * t
+        grad_out = grad_out.to(v.dtype).contiguous()
+        dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+        dq = torch.empty_like(queries)
+        lib = _lib.lib()
+        dt = _lib.dtype_code(v.dtype)
+        with torch.cuda.device(v.device):
+            ws_bytes = lib.sy_bwd_batched_workspace_bytes(n, s, n_tok, d, dt)
+            if ws_bytes < 0:
+                _lib.check(int(ws_bytes), "sy_bwd_batched_workspace_bytes")
+            ws = torch.empty(max(1, (ws_bytes + 3) // 4), device=v.device, dtype=torch.float32)
+            rc = lib.sy_bwd_batched(
+                _ptr(v), _ptr(queries), _ptr(grad_out), _ptr(dv), _ptr(dq), _ptr(ws), ws.numel() * 4,
+                n, s, n_tok, d, n_tok * d, dt, ctx.eps, _lib.stream_ptr(v.device),
+            )
+        _lib.check(rc, "sy_bwd_batched")
+        return dv, dq, None
+
+
+def block_attn_res_batched_train(
+    v: torch.Tensor, queries: torch.Tensor, eps: float = DEFAULT_EPS
+) -> torch.Tensor:
+    """``block_attn_res_batched`` with a backward: ``out[s] = AttnRes(v, queries[s])``.
+
+    The reference's batched API is output-only and raises under autograd
+    (triton_op.py:463-467, kept as is in ``block_attn_res_batched``); this is
+    its training contract. Forward: the same single read of ``v`` for all
+    queries. Backward: one persistent kernel reads ``v`` and the ``S``
+    output gradients once, writes ``dv = sum_s dv_s`` rounded once and fp32
+    per-workgroup ``dq`` partials, then the fixed-order reduction writes
+    ``dq`` -- two kernels, bit-reproducible.
+    """
+    return _BlockAttnResBatched.apply(v, queries, eps)
+
+
+def block_attn_res_batched(
+    v: torch.Tensor, queries: torch.Tensor, eps: float = DEFAULT_EPS
+) -> torch.Tensor:
+    """``S`` pseudo-queries against one shared read of ``v`` (output only).
+
+    Same contract as the reference's ``block_attn_res_batched``
+    (triton_op.py:438-501): ``out[s] == block_attn_res_triton(v, queries[s])``,
+    ``[S, B, T, D]``, no backward. For N, D, dtype the resident kernel holds
+    and S <= 16 one kernel reads ``v`` once; other shapes issue one forward
+    launch per query, written straight into ``out[s]`` (no stack).
+    """
+    _validate_batched(v, queries)
+    if v.requires_grad or queries.requires_grad:
+        raise RuntimeError(
+            "block_attn_res_batched has no backward; use block_attn_res_triton per query "
+            "for training, or run this under torch.no_grad() for inference"
+        )
+    return _batched_forward(v.contiguous(), queries.contiguous(), eps)
 
 
 class BlockAttnResHIP(torch.nn.Module):

@@ -16,6 +16,10 @@
  *   dv       [N][n_tok][D]  contiguous (source stride n_tok*D)
  *   w, dw    [D]
  *   queries  [S][D], batched out [S][n_tok][D]
+ *   m, l     [n_tok] fp32 (batched: [S][n_tok]): max logit, sum of exp(logit - m)
+ * The *_table entry points take the sources as a host array of N device
+ * pointers instead, each source [n_tok][D] contiguous (dv likewise), so
+ * separately allocated sources need no stacking copy.
  * n_tok is B*T: the batch and sequence axes are flattened because tokens are
  * independent.
  *
@@ -38,7 +42,10 @@
 extern "C" {
 #endif
 
-#define SY_ABI_VERSION 1
+#define SY_ABI_VERSION 2
+
+/* Most sources a per-source pointer list (the *_table entry points) may hold. */
+#define SY_MAX_TABLE_ROWS 16
 
 /* Element types. Reference: tensors may be bf16/fp16/fp32 and all arithmetic is
  * fp32 (src/switchyard/triton_op.py:36, :66-67). */
@@ -56,7 +63,13 @@ typedef enum sy_status {
 } sy_status;
 
 /* Operations known to sy_plan(). */
-typedef enum sy_op { SY_OP_FWD = 0, SY_OP_BWD = 1, SY_OP_BATCHED = 2, SY_OP_SOL = 3 } sy_op;
+typedef enum sy_op {
+  SY_OP_FWD = 0,
+  SY_OP_BWD = 1,
+  SY_OP_BATCHED = 2,
+  SY_OP_SOL = 3,
+  SY_OP_BWD_BATCHED = 4
+} sy_op;
 
 /* Kernel families a plan can select. */
 typedef enum sy_family {
@@ -95,6 +108,40 @@ int sy_plan_for(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int 
 int sy_fwd(const void* v, const void* w, void* out, float* stats, int64_t n_src, int64_t n_tok,
            int64_t d, int64_t src_stride, int v_dtype, int w_dtype, float eps, void* stream);
 
+/* sy_fwd with the sources given as a host array of n_src <= SY_MAX_TABLE_ROWS
+ * device pointers, v_rows[n] -> [n_tok][D]. The reference takes only a stacked
+ * tensor and names a per-source pointer table (fla's API) as the better design
+ * that removes the stacking copy (docs/report.md:401-404); this is that input.
+ * SY_ERR_SHAPE when n_src > SY_MAX_TABLE_ROWS, SY_ERR_NULL for a NULL row. */
+int sy_fwd_table(const void* const* v_rows, const void* w, void* out, float* stats, int64_t n_src,
+                 int64_t n_tok, int64_t d, int v_dtype, int w_dtype, float eps, void* stream);
+
+/* attn_with_stats: the unnormalised partial result of one source group,
+ *     m = max_n logit_n,  l = sum_n exp(logit_n - m),  o = sum_n exp(logit_n - m) v_n,
+ * so that o / l is the operator's output and two groups merge exactly with
+ * sy_merge_stats. o has v's dtype; m and l are fp32 [n_tok]; stats as in sy_fwd.
+ * Replaces attn_with_stats (src/switchyard/reference.py:194-215). */
+int sy_attn_with_stats(const void* v, const void* w, void* o, float* m, float* l, float* stats,
+                       int64_t n_src, int64_t n_tok, int64_t d, int64_t src_stride, int v_dtype,
+                       int w_dtype, float eps, void* stream);
+
+/* Merge two (o, m, l) results of disjoint source groups into their union:
+ * m = max(m1, m2), s_i = exp(m_i - m), o = s1 o1 + s2 o2, l = s1 l1 + s2 l2.
+ * o may alias o1 or o2 (and m/l likewise). Replaces merge_online_softmax
+ * (src/switchyard/reference.py:218-233). */
+int sy_merge_stats(const void* o1, const float* m1, const float* l1, const void* o2,
+                   const float* m2, const float* l2, void* o, float* m, float* l, int64_t n_tok,
+                   int64_t d, int dtype, void* stream);
+
+/* Gradient of sy_merge_stats: from dL/d(o, m, l) to dL/d(o1, m1, l1) and
+ * dL/d(o2, m2, l2). The max goes to group 1 on a tie. Outputs must not alias
+ * inputs. No reference counterpart (the reference merge is forward-only);
+ * it completes the two-phase schedule's training path. */
+int sy_merge_stats_bwd(const void* o1, const float* m1, const float* l1, const void* o2,
+                       const float* m2, const float* l2, const void* grad_o, const float* grad_m,
+                       const float* grad_l, void* do1, float* dm1, float* dl1, void* do2,
+                       float* dm2, float* dl2, int64_t n_tok, int64_t d, int dtype, void* stream);
+
 /* Bytes of device workspace sy_bwd needs for this shape on the current device
  * (per-workgroup fp32 dw partials). Returns < 0 (an sy_status) on bad input.
  * Replaces the fp32 dw buffer of triton_op.py:550. */
@@ -109,6 +156,26 @@ int64_t sy_bwd_workspace_bytes(int64_t n_src, int64_t n_tok, int64_t d, int v_dt
 int sy_bwd(const void* v, const void* w, const void* grad_out, const float* stats, void* dv,
            void* dw, void* workspace, int64_t workspace_bytes, int64_t n_src, int64_t n_tok,
            int64_t d, int64_t src_stride, int v_dtype, int w_dtype, float eps, void* stream);
+
+/* sy_bwd over per-source pointer lists: v_rows and dv_rows each hold n_src <=
+ * SY_MAX_TABLE_ROWS device pointers to [n_tok][D] rows (dv rows must not
+ * overlap). Same workspace as sy_bwd. Pointer-table input as for sy_fwd_table. */
+int sy_bwd_table(const void* const* v_rows, const void* w, const void* grad_out,
+                 const float* stats, void* const* dv_rows, void* dw, void* workspace,
+                 int64_t workspace_bytes, int64_t n_src, int64_t n_tok, int64_t d, int v_dtype,
+                 int w_dtype, float eps, void* stream);
+
+/* Gradient of sy_attn_with_stats: from grad_o (v dtype [n_tok][D]) and grad_m,
+ * grad_l (fp32 [n_tok]) to dv and dw, with k the first row holding the max:
+ *     dlogit_n = p_n (G_n + grad_l) (n != k),  dlogit_k = grad_m - sum_{n != k} p_n (G_n + grad_l),
+ *     p_n = exp(logit_n - m), G_n = <grad_o, v_n>, then dv, dw as in sy_bwd with
+ *     p_n in place of alpha_n. Same workspace and stats as sy_bwd. The reference
+ * has no backward for attn_with_stats (src/switchyard/reference.py:194-215). */
+int sy_attn_with_stats_bwd(const void* v, const void* w, const void* grad_o, const float* grad_m,
+                           const float* grad_l, const float* stats, void* dv, void* dw,
+                           void* workspace, int64_t workspace_bytes, int64_t n_src, int64_t n_tok,
+                           int64_t d, int64_t src_stride, int v_dtype, int w_dtype, float eps,
+                           void* stream);
 
 /* The two stages of sy_bwd, separately launchable (to time them, or to run the
  * small dw reduction later on another stream). sy_bwd == sy_bwd_main followed
@@ -131,6 +198,37 @@ int sy_dw_reduce(const float* partial, int64_t rows, int64_t d, void* dw, int w_
  * Replaces block_attn_res_batched/_fwd_batched_resident
  * (src/switchyard/triton_op.py:438-501, :378-414). */
 int sy_fwd_batched(const void* v, const void* queries, void* out, int64_t n_src, int64_t n_q,
+                   int64_t n_tok, int64_t d, int64_t src_stride, int dtype, float eps,
+                   void* stream);
+
+/* sy_fwd_batched over a per-source pointer list (see sy_fwd_table). */
+int sy_fwd_batched_table(const void* const* v_rows, const void* queries, void* out, int64_t n_src,
+                         int64_t n_q, int64_t n_tok, int64_t d, int dtype, float eps,
+                         void* stream);
+
+/* Batched attn_with_stats: o[s] (v dtype [S][n_tok][D], unnormalised), m[s] and
+ * l[s] (fp32 [S][n_tok]) for S queries sharing one read of v -- the batched
+ * inter-block phase of the two-phase schedule, returning the merge statistics
+ * the reference's batched API lacks (src/switchyard/reference.py:194-215,
+ * triton_op.py:438-501). */
+int sy_batched_with_stats(const void* v, const void* queries, void* o, float* m, float* l,
+                          int64_t n_src, int64_t n_q, int64_t n_tok, int64_t d, int64_t src_stride,
+                          int dtype, float eps, void* stream);
+
+/* Bytes of workspace sy_bwd_batched needs (fp32 dq partials, one row of
+ * n_q*D per workgroup of its persistent grid), or < 0 on bad input. */
+int64_t sy_bwd_batched_workspace_bytes(int64_t n_src, int64_t n_q, int64_t n_tok, int64_t d,
+                                       int dtype);
+
+/* Backward of the batched forward: from grad_out [S][n_tok][D] (v dtype) to
+ * dv (contiguous [N][n_tok][D]) = sum over queries of each query's source
+ * gradient, and dq [S][D] (v dtype) = each query's pseudo-query gradient,
+ * reduced over tokens in a fixed order (no float atomics). v is read once
+ * for all S queries and dv is rounded once. The reference's batched API has no
+ * backward (src/switchyard/triton_op.py:438-501, PROJECT_STATE.md:74-76 lists
+ * it as next); this completes its training contract. */
+int sy_bwd_batched(const void* v, const void* queries, const void* grad_out, void* dv, void* dq,
+                   void* workspace, int64_t workspace_bytes, int64_t n_src, int64_t n_q,
                    int64_t n_tok, int64_t d, int64_t src_stride, int dtype, float eps,
                    void* stream);
 

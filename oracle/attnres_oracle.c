@@ -176,3 +176,108 @@ int oracle_batched(const double* v, const double* q, double* out, int64_t n, int
   }
   return 0;
 }
+
+/* Gradient of attn_with_stats for upstream (go [T][D], gm [T], gl [T]).
+ * Derivation (no reference counterpart; written from reference.py:195-216):
+ * with k the first row holding the max logit m, p_i = exp(logit_i - m) and
+ * G_i = <go, v_i>, the loss depends on logit_i through p_i (o and ell) and,
+ * for i = k, through m itself:
+ *   dlogit_i = p_i (G_i + gl)                           i != k
+ *   dlogit_k = gm - sum_{i != k} p_i (G_i + gl)         (p_k = 1)
+ * and the chain through logit_i = r_i <w, v_i> is the one of oracle_backward,
+ * with p_i in place of alpha_i in the direct term p_i * go. */
+int oracle_attn_with_stats_backward(const double* v, const double* w, const double* go,
+                                    const double* gm, const double* gl, double* dv, double* dw,
+                                    int64_t n, int64_t t, int64_t d, double eps) {
+  if (n < 1 || t < 0 || d < 1) return -1;
+  double* buf = (double*)malloc(sizeof(double) * 4 * (size_t)n);
+  if (!buf) return -2;
+  double *logit = buf, *p = buf + n, *rinv = buf + 2 * n, *dlg = buf + 3 * n;
+  for (int64_t k = 0; k < d; ++k) dw[k] = 0.0;
+  for (int64_t tok = 0; tok < t; ++tok) {
+    token_alpha(v, w, n, t, tok, d, eps, logit, p, rinv);
+    int64_t top = 0;
+    for (int64_t i = 1; i < n; ++i)
+      if (logit[i] > logit[top]) top = i;
+    const double* gt = go + tok * d;
+    double other = 0.0;
+    for (int64_t i = 0; i < n; ++i) {
+      const double* x = v + (i * t + tok) * d;
+      double gg = 0.0;
+      for (int64_t k = 0; k < d; ++k) gg += gt[k] * x[k];
+      p[i] = exp(logit[i] - logit[top]);
+      dlg[i] = p[i] * (gg + gl[tok]);
+      if (i != top) other += dlg[i];
+    }
+    dlg[top] = gm[tok] - other;
+    for (int64_t i = 0; i < n; ++i) {
+      const double* x = v + (i * t + tok) * d;
+      double* dx = dv + (i * t + tok) * d;
+      const double r = rinv[i];
+      const double a = logit[i] / r;
+      const double da = dlg[i] * r;
+      const double dssq = -dlg[i] * a * r * r * r / (2.0 * (double)d);
+      for (int64_t k = 0; k < d; ++k) {
+        dx[k] = p[i] * gt[k] + da * w[k] + 2.0 * dssq * x[k];
+        dw[k] += da * x[k];
+      }
+    }
+  }
+  free(buf);
+  return 0;
+}
+
+/* Gradient of oracle_merge for upstream (go [T][D], gm [T], gl [T]). With
+ * s_i = exp(m_i - m) and k the group holding the max (group 1 on a tie):
+ *   do_i = s_i go, dl_i = s_i gl, ds_i = <go, o_i> + gl l_i,
+ *   dm_j = s_j ds_j for the other group j, dm_k = gm - s_j ds_j. */
+void oracle_merge_backward(const double* o1, const double* m1, const double* l1, const double* o2,
+                           const double* m2, const double* l2, const double* go, const double* gm,
+                           const double* gl, double* do1, double* dm1, double* dl1, double* do2,
+                           double* dm2, double* dl2, int64_t t, int64_t d) {
+  for (int64_t tok = 0; tok < t; ++tok) {
+    const int first = m1[tok] >= m2[tok];
+    const double mm = first ? m1[tok] : m2[tok];
+    const double s1 = exp(m1[tok] - mm), s2 = exp(m2[tok] - mm);
+    double d1 = 0.0, d2 = 0.0;
+    for (int64_t k = 0; k < d; ++k) {
+      const double g = go[tok * d + k];
+      d1 += g * o1[tok * d + k];
+      d2 += g * o2[tok * d + k];
+      do1[tok * d + k] = s1 * g;
+      do2[tok * d + k] = s2 * g;
+    }
+    const double ds1 = d1 + gl[tok] * l1[tok], ds2 = d2 + gl[tok] * l2[tok];
+    dl1[tok] = s1 * gl[tok];
+    dl2[tok] = s2 * gl[tok];
+    if (first) {
+      dm2[tok] = s2 * ds2;
+      dm1[tok] = gm[tok] - s2 * ds2;
+    } else {
+      dm1[tok] = s1 * ds1;
+      dm2[tok] = gm[tok] - s1 * ds1;
+    }
+  }
+}
+
+/* Gradient of oracle_batched for upstream g [S][T][D]: the S queries are S
+ * independent operators sharing v, so dv = sum_s dv_s and dq[s] = dw_s of
+ * oracle_backward(v, q[s], g[s]). dv [N][T][D], dq [S][D]. */
+int oracle_batched_backward(const double* v, const double* q, const double* g, double* dv,
+                            double* dq, int64_t n, int64_t s, int64_t t, int64_t d, double eps) {
+  if (n < 1 || s < 1 || t < 0 || d < 1) return -1;
+  const size_t vol = (size_t)n * (size_t)t * (size_t)d;
+  double* tmp = (double*)malloc(sizeof(double) * (vol > 0 ? vol : 1));
+  if (!tmp) return -2;
+  for (size_t k = 0; k < vol; ++k) dv[k] = 0.0;
+  for (int64_t i = 0; i < s; ++i) {
+    const int rc = oracle_backward(v, q + i * d, g + i * t * d, tmp, dq + i * d, n, t, d, eps);
+    if (rc) {
+      free(tmp);
+      return rc;
+    }
+    for (size_t k = 0; k < vol; ++k) dv[k] += tmp[k];
+  }
+  free(tmp);
+  return 0;
+}

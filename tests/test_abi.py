@@ -26,7 +26,7 @@ def declared_functions() -> list[str]:
 def test_library_exports_every_declared_symbol():
     lib = _lib.lib()
     names = declared_functions()
-    assert len(names) >= 14, names
+    assert len(names) >= 24, names
     for name in names:
         assert hasattr(lib, name), f"{name} declared in switchyard.h but not exported"
     assert set(names) == set(_lib.SIGNATURES), "ctypes table and header disagree"
@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_strings():
     lib = _lib.lib()
-    assert lib.sy_abi_version() == 1
+    assert lib.sy_abi_version() == 2
     for code in (OK, NULL, SHAPE, DTYPE, WORKSPACE, STRIDE, DEVICE, OP):
         assert lib.sy_strerror(code)
     assert b"NULL" in lib.sy_strerror(NULL)
@@ -91,6 +91,58 @@ def test_backward_and_batched_reject_bad_arguments():
     assert lib.sy_bwd_workspace_bytes(9, 16, 2048, 5, BF16) == DTYPE
     assert lib.sy_bwd_workspace_bytes(9, 0, 2048, BF16, BF16) == 0
     assert lib.sy_bwd_partial_rows(9, 0, 2048, BF16, BF16, 1, 1) == 0
+
+
+def _table(*ptrs):
+    return (ctypes.c_void_p * len(ptrs))(*ptrs)
+
+
+def test_pointer_table_entry_points_reject_bad_arguments():
+    lib = _lib.lib()
+    rows = _table(FAKE, FAKE)
+    # NULL table, NULL row, too many rows, bad dtype, bad size
+    assert lib.sy_fwd_table(None, _p(FAKE), _p(FAKE), None, 2, 16, 2048, BF16, BF16, 1e-6, None) == NULL
+    assert lib.sy_fwd_table(_table(FAKE, None), _p(FAKE), _p(FAKE), None, 2, 16, 2048, BF16, BF16,
+                            1e-6, None) == NULL
+    big = _table(*([FAKE] * 17))
+    assert lib.sy_fwd_table(big, _p(FAKE), _p(FAKE), None, 17, 16, 2048, BF16, BF16, 1e-6, None) == SHAPE
+    assert lib.sy_fwd_table(rows, _p(FAKE), _p(FAKE), None, 2, 16, 2048, 9, BF16, 1e-6, None) == DTYPE
+    assert lib.sy_fwd_table(rows, _p(FAKE), _p(FAKE), None, 2, 16, 0, BF16, BF16, 1e-6, None) == SHAPE
+    assert lib.sy_fwd_table(None, None, None, None, 2, 0, 2048, BF16, BF16, 1e-6, None) == OK
+    assert lib.sy_bwd_table(rows, _p(FAKE), _p(FAKE), None, rows, None, _p(FAKE), 1 << 20, 2, 16, 2048,
+                            BF16, BF16, 1e-6, None) == NULL
+    assert lib.sy_bwd_table(rows, _p(FAKE), _p(FAKE), None, _table(FAKE, None), _p(FAKE), _p(FAKE),
+                            1 << 20, 2, 16, 2048, BF16, BF16, 1e-6, None) == NULL
+    assert lib.sy_fwd_batched_table(rows, _p(FAKE), _p(FAKE), 2, 0, 16, 2048, BF16, 1e-6, None) == SHAPE
+
+
+def test_statistics_and_merge_entry_points_reject_bad_arguments():
+    lib = _lib.lib()
+    f = _p(FAKE)
+    assert lib.sy_attn_with_stats(f, f, f, None, f, None, 9, 16, 2048, 16 * 2048, BF16, BF16, 1e-6,
+                                  None) == NULL
+    assert lib.sy_attn_with_stats(f, f, f, f, f, None, 9, 16, 2048, 100, BF16, BF16, 1e-6, None) == STRIDE
+    assert lib.sy_attn_with_stats_bwd(f, f, f, None, f, None, f, f, f, 1 << 20, 9, 16, 2048, 16 * 2048,
+                                      BF16, BF16, 1e-6, None) == NULL
+    assert lib.sy_batched_with_stats(f, f, f, f, f, 9, 0, 16, 2048, 16 * 2048, BF16, 1e-6, None) == SHAPE
+    assert lib.sy_merge_stats(f, f, f, f, f, f, f, f, f, 16, 2048, 7, None) == DTYPE
+    assert lib.sy_merge_stats(f, f, f, f, f, f, f, f, f, 16, 0, BF16, None) == SHAPE
+    assert lib.sy_merge_stats(f, f, None, f, f, f, f, f, f, 16, 2048, BF16, None) == NULL
+    assert lib.sy_merge_stats(None, None, None, None, None, None, None, None, None, 0, 2048, BF16,
+                              None) == OK
+    assert lib.sy_merge_stats_bwd(*([f] * 14), None, 16, 2048, BF16, None) == NULL
+
+
+def test_batched_backward_rejects_bad_arguments():
+    lib = _lib.lib()
+    f = _p(FAKE)
+    assert lib.sy_bwd_batched(f, f, f, f, None, f, 1 << 20, 9, 8, 16, 2048, 16 * 2048, BF16, 1e-6,
+                              None) == NULL
+    assert lib.sy_bwd_batched(f, f, f, f, f, f, 1 << 20, 9, 0, 16, 2048, 16 * 2048, BF16, 1e-6,
+                              None) == SHAPE
+    assert lib.sy_bwd_batched(f, f, f, f, f, f, 1 << 20, 9, 8, 16, 2048, 100, BF16, 1e-6, None) == STRIDE
+    assert lib.sy_bwd_batched_workspace_bytes(9, 0, 16, 2048, BF16) == SHAPE
+    assert lib.sy_bwd_batched_workspace_bytes(9, 8, 0, 2048, BF16) == 0
 
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-device status")
@@ -174,10 +226,28 @@ def test_backward_never_takes_a_four_chunk_tile():
                 assert p["tokens_per_block"] * p["waves_per_token"] == 8
 
 
+def test_batched_backward_plan():
+    # one chunk per lane on the fewest waves that cover the row; N <= 9, S <= 8
+    p = plan(_lib.OP_BWD_BATCHED, 9, 2048, n_q=8)
+    assert (p["family_name"], p["waves_per_token"], p["chunks_per_lane"], p["rows_per_tile"]) == \
+        ("resident", 4, 1, 9)
+    assert plan(_lib.OP_BWD_BATCHED, 4, 4096, n_q=3)["waves_per_token"] == 8
+    assert plan(_lib.OP_BWD_BATCHED, 4, 512, n_q=3)["rows_per_tile"] == 4
+    assert plan(_lib.OP_BWD_BATCHED, 9, 2048, torch.float32, n_q=2)["waves_per_token"] == 8
+    for n, s, d in ((10, 8, 2048), (9, 9, 2048), (9, 8, 8192), (5, 3, 777)):
+        assert plan(_lib.OP_BWD_BATCHED, n, d, n_q=s)["family_name"] == "generic", (n, s, d)
+    assert plan(_lib.OP_BWD_BATCHED, 9, 2048, n_q=8, aligned=False)["family_name"] == "generic"
+    p = _lib.Plan()
+    # the generic kernel's per-(query, source) scalars must fit its LDS
+    assert _lib.lib().sy_plan_for(4, 4096, 8, 2048, BF16, BF16, 1, ctypes.byref(p)) == SHAPE
+    assert _lib.lib().sy_plan_for(4, 9, 0, 2048, BF16, BF16, 1, ctypes.byref(p)) == SHAPE
+
+
 def test_planner_rejects_bad_input():
     p = _lib.Plan()
     lib = _lib.lib()
     assert lib.sy_plan_for(9, 9, 0, 2048, BF16, BF16, 1, ctypes.byref(p)) == OP
+    assert lib.sy_plan_for(5, 9, 1, 2048, BF16, BF16, 1, ctypes.byref(p)) == OP
     assert lib.sy_plan_for(0, 0, 0, 2048, BF16, BF16, 1, ctypes.byref(p)) == SHAPE
     assert lib.sy_plan_for(2, 9, 0, 2048, BF16, BF16, 1, ctypes.byref(p)) == SHAPE
     assert lib.sy_plan_for(0, 9, 0, 2048, 3, BF16, 1, ctypes.byref(p)) == DTYPE

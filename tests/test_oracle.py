@@ -457,3 +457,134 @@ def test_planted_backward_mistakes_are_caught(mutation):
         return _bwd_np(v, w, g, **{mutation: True})
 
     assert _failed_pins(_fwd_np, bwd), f"{mutation} slipped past every pin"
+
+
+# --------------------------------------------------------------------------
+# 6. Merge statistics, the merge and the batched operator: gradients
+#    (no reference counterpart; pinned by f64 autograd, gradcheck and central
+#    differences of the already-pinned forwards)
+# --------------------------------------------------------------------------
+
+
+def _stats_loss(v, w, go, gm, gl):
+    o, m, ell = c_oracle.attn_with_stats(v, w)
+    return float(np.sum(o * go) + np.sum(m * gm) + np.sum(ell * gl))
+
+
+def _stats_case(seed=11, n=5, t=4, d=12, scale=1.5):
+    rng = np.random.default_rng(seed)
+    v = rng.standard_normal((n, t, d))
+    w = rng.standard_normal(d) * scale
+    go = rng.standard_normal((t, d))
+    gm, gl = rng.standard_normal(t), rng.standard_normal(t)
+    return v, w, go, gm, gl
+
+
+def _stats_bwd_np(v, w, go, gm, gl, drop_gm=False, normalized=False, keep_top=False):
+    """numpy restatement of oracle_attn_with_stats_backward with plantable mistakes."""
+    n, t, d = v.shape
+    ssq = np.einsum("ntd,ntd->nt", v, v)
+    r = 1.0 / np.sqrt(ssq / d + DEFAULT_EPS)
+    a = np.einsum("d,ntd->nt", w, v)
+    logit = a * r
+    top = logit.argmax(0)
+    p = np.exp(logit - logit.max(0))
+    if normalized:
+        p = p / p.sum(0)
+    dl = p * (np.einsum("td,ntd->nt", go, v) + gl)
+    other = dl.sum(0) - (0.0 if keep_top else dl[top, np.arange(t)])
+    dl[top, np.arange(t)] = (0.0 if drop_gm else gm) - other
+    da = dl * r
+    dssq = -dl * a * r**3 / (2 * d)
+    dv = p[..., None] * go[None] + da[..., None] * w + 2 * dssq[..., None] * v
+    return dv, np.einsum("nt,ntd->d", da, v)
+
+
+def _stats_pins_fail(bwd) -> list[str]:
+    failed = []
+    v, w, go, gm, gl = _stats_case()
+    dv, dw = bwd(v, w, go, gm, gl)
+    h = 1e-6
+    for idx in [(0, 0, 0), (2, 1, 5), (4, 3, 11)]:
+        vp, vm = v.copy(), v.copy()
+        vp[idx] += h
+        vm[idx] -= h
+        fd = (_stats_loss(vp, w, go, gm, gl) - _stats_loss(vm, w, go, gm, gl)) / (2 * h)
+        if abs(fd - dv[idx]) > 1e-6 * max(1.0, abs(fd)):
+            failed.append(f"dv{idx}")
+    for k in (0, 7):
+        wp, wm = w.copy(), w.copy()
+        wp[k] += h
+        wm[k] -= h
+        fd = (_stats_loss(v, wp, go, gm, gl) - _stats_loss(v, wm, go, gm, gl)) / (2 * h)
+        if abs(fd - dw[k]) > 1e-6 * max(1.0, abs(fd)):
+            failed.append(f"dw{k}")
+    return failed
+
+
+def test_c_stats_backward_passes_central_differences():
+    assert _stats_pins_fail(c_oracle.attn_with_stats_backward) == []
+    assert _stats_pins_fail(_stats_bwd_np) == []
+
+
+@pytest.mark.parametrize("mutation", ["drop_gm", "normalized", "keep_top"])
+def test_planted_stats_backward_mistakes_are_caught(mutation):
+    def bwd(*a):
+        return _stats_bwd_np(*a, **{mutation: True})
+
+    assert _stats_pins_fail(bwd), f"{mutation} slipped past every pin"
+
+
+def test_torch_stats_and_merge_pass_gradcheck():
+    torch.manual_seed(5)
+    v = torch.randn(4, 1, 3, 6, **F64, requires_grad=True)
+    w = torch.randn(6, **F64, requires_grad=True)
+    assert torch.autograd.gradcheck(lambda a, b: attn_with_stats(a, b), (v, w), eps=1e-6,
+                                    atol=1e-8, rtol=1e-6)
+    o1, o2 = (torch.randn(3, 5, **F64, requires_grad=True) for _ in range(2))
+    m1 = torch.tensor([0.3, -1.0, 2.0], **F64, requires_grad=True)
+    m2 = torch.tensor([-0.4, 0.5, 1.2], **F64, requires_grad=True)
+    l1, l2 = (torch.rand(3, **F64).add(0.5).requires_grad_() for _ in range(2))
+    assert torch.autograd.gradcheck(merge_online_softmax, (o1, m1, l1, o2, m2, l2), eps=1e-6,
+                                    atol=1e-8, rtol=1e-6)
+
+
+def test_c_stats_backward_matches_autograd():
+    v, w, go, gm, gl = _stats_case(seed=21, n=7, t=6, d=20, scale=3.0)
+    vt = torch.tensor(v, requires_grad=True)
+    wt = torch.tensor(w, requires_grad=True)
+    o, m, ell = attn_with_stats(vt[:, None], wt)
+    loss = (o[0] * torch.tensor(go)).sum() + (m[0] * torch.tensor(gm)).sum() + (ell[0] * torch.tensor(gl)).sum()
+    gv, gw = torch.autograd.grad(loss, (vt, wt))
+    dv, dw = c_oracle.attn_with_stats_backward(v, w, go, gm, gl)
+    np.testing.assert_allclose(dv, gv.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dw, gw.numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_c_merge_backward_matches_autograd():
+    rng = np.random.default_rng(8)
+    t, d = 6, 9
+    o1, o2, go = (rng.standard_normal((t, d)) for _ in range(3))
+    m1 = np.array([0.1, 2.0, -1.0, 0.7, 3.0, -2.0])
+    m2 = np.array([1.1, 0.5, -0.5, 0.2, 4.0, -3.0])  # group 2 wins some tokens, group 1 others
+    l1, l2 = rng.random(t) + 0.5, rng.random(t) + 0.5
+    gm, gl = rng.standard_normal(t), rng.standard_normal(t)
+    ins = [torch.tensor(a, requires_grad=True) for a in (o1, m1, l1, o2, m2, l2)]
+    o, m, ell = merge_online_softmax(*ins)
+    loss = (o * torch.tensor(go)).sum() + (m * torch.tensor(gm)).sum() + (ell * torch.tensor(gl)).sum()
+    want = torch.autograd.grad(loss, ins)
+    got = c_oracle.merge_backward(o1, m1, l1, o2, m2, l2, go, gm, gl)  # same input order
+    for g, ref in zip(got, want):
+        np.testing.assert_allclose(g, ref.numpy(), rtol=1e-12, atol=1e-12)
+
+
+def test_c_batched_backward_matches_autograd_of_the_batched_form():
+    v, _ = _inputs(n=5, b=1, t=4, d=16, seed=13)
+    q = (torch.randn(3, 16, **F64) * 0.7)
+    g = torch.randn(3, 1, 4, 16, **F64)
+    vt, qt = v.clone().requires_grad_(), q.clone().requires_grad_()
+    out = batched_folded_form(vt, qt)
+    gv, gq = torch.autograd.grad((out * g).sum(), (vt, qt))
+    dv, dq = c_oracle.batched_backward(v[:, 0].numpy(), q.numpy(), g[:, 0].numpy())
+    np.testing.assert_allclose(dv, gv[:, 0].numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dq, gq.numpy(), rtol=1e-10, atol=1e-12)

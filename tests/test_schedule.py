@@ -1,0 +1,265 @@
+"""Merge statistics, the two-phase schedule and the batched backward (GPU),
+against the float64 C oracle.
+
+Bars: bf16/fp16 results rounded once from fp32 accumulation are within 1.10x
+of the dtype floor (``||round(oracle) - oracle|| / ||oracle||``), like the
+operator itself; fp32 tensors and the fp32 statistics ``m``, ``l`` within
+1e-5 relative L2. The two-phase composition rounds three times (each
+group's ``o``, the merged ``o``, the output), so its bf16/fp16 bound is 2.5x
+the floor; in fp32 it is 1e-5.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+if not torch.cuda.is_available():  # pragma: no cover
+    pytest.skip("needs a HIP device", allow_module_level=True)
+
+from oracle import c_oracle  # noqa: E402
+from oracle.reference import DEFAULT_EPS, dtype_floor, rel_l2  # noqa: E402
+from switchyard import _lib  # noqa: E402
+from switchyard.stats_op import (  # noqa: E402
+    attn_with_stats,
+    block_attn_res_batched_with_stats,
+    block_attn_res_two_phase,
+    merge_online_softmax,
+)
+from switchyard.hip_op import block_attn_res_batched_train  # noqa: E402
+from switchyard.triton_op import block_attn_res_batched, block_attn_res_triton  # noqa: E402
+
+DEV = "cuda"
+DTYPES = [torch.bfloat16, torch.float16, torch.float32]
+
+
+def _bound(oracle, dtype, mult=1.10):
+    return 1e-5 if dtype == torch.float32 else max(mult * dtype_floor(oracle, dtype), 1e-6)
+
+
+def _close(got, oracle, dtype, mult=1.10, what=""):
+    oracle = torch.as_tensor(oracle)
+    err = rel_l2(got, oracle)
+    assert err <= _bound(oracle, dtype, mult), f"{what}: rel_l2 {err:.3e}, floor {dtype_floor(oracle, dtype):.3e}"
+
+
+def _stat_close(got, oracle, what=""):
+    err = rel_l2(got, torch.as_tensor(oracle))
+    assert err <= 1e-5, f"{what}: rel_l2 {err:.3e}"
+
+
+def _make(n, t, d, dtype, seed=0, scale=4.0):
+    g = torch.Generator().manual_seed(seed)
+    v = torch.randn(n, 1, t, d, generator=g).to(dtype)
+    w = torch.randn(d, generator=g)
+    w = (w / w.norm() * scale).to(dtype)
+    return v.to(DEV), w.to(DEV)
+
+
+def _np(x):
+    return x.detach().double().cpu().numpy()
+
+
+SHAPES = [(1, 32, 256), (4, 64, 512), (9, 128, 2048), (16, 40, 1024), (5, 33, 777), (20, 16, 512)]
+
+
+# -- attn_with_stats ---------------------------------------------------------
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_attn_with_stats_forward(shape, dtype):
+    n, t, d = shape
+    print(f"stats fwd {shape} {dtype}", flush=True)
+    v, w = _make(n, t, d, dtype, seed=1)
+    o, m, ell = attn_with_stats(v, w)
+    ro, rm, rl = c_oracle.attn_with_stats(_np(v)[:, 0], _np(w))
+    _close(o[0].cpu(), ro, dtype, what="o")
+    _stat_close(m[0].cpu(), rm, "m")
+    _stat_close(ell[0].cpu(), rl, "l")
+    # o / l is the operator (same kernel family, one more rounding of o)
+    _close((o.float() / ell.unsqueeze(-1)).to(dtype)[0].cpu(),
+           c_oracle.forward(_np(v)[:, 0], _np(w)), dtype, mult=2.5, what="o/l")
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_attn_with_stats_backward(shape, dtype):
+    n, t, d = shape
+    print(f"stats bwd {shape} {dtype}", flush=True)
+    v, w = _make(n, t, d, dtype, seed=2)
+    gen = torch.Generator().manual_seed(9)
+    go = torch.randn(1, t, d, generator=gen).to(dtype).to(DEV)
+    gm = torch.randn(1, t, generator=gen).to(DEV)
+    gl = torch.randn(1, t, generator=gen).to(DEV)
+    vv, ww = v.clone().requires_grad_(), w.clone().requires_grad_()
+    o, m, ell = attn_with_stats(vv, ww)
+    torch.autograd.backward((o, m, ell), (go, gm, gl))
+    rdv, rdw = c_oracle.attn_with_stats_backward(_np(v)[:, 0], _np(w), _np(go)[0], _np(gm)[0], _np(gl)[0])
+    _close(vv.grad[:, 0].cpu(), rdv, dtype, what="dv")
+    _close(ww.grad.cpu(), rdw, dtype, what="dw")
+
+
+def test_attn_with_stats_backward_with_unused_outputs():
+    """Only o feeds the loss: m and l get no gradient (zeros are substituted)."""
+    v, w = _make(9, 64, 2048, torch.bfloat16, seed=3)
+    go = torch.randn(1, 64, 2048, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).to(DEV)
+    vv = v.clone().requires_grad_()
+    o, _, _ = attn_with_stats(vv, w)
+    o.backward(go)
+    zeros = np.zeros(64)
+    rdv, _ = c_oracle.attn_with_stats_backward(_np(v)[:, 0], _np(w), _np(go)[0], zeros, zeros)
+    _close(vv.grad[:, 0].cpu(), rdv, torch.bfloat16, what="dv")
+
+
+# -- merge -------------------------------------------------------------------
+
+
+def _merge_inputs(t, d, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    o1 = torch.randn(1, t, d, generator=g).to(dtype).to(DEV)
+    o2 = torch.randn(1, t, d, generator=g).to(dtype).to(DEV)
+    m1 = (torch.randn(1, t, generator=g) * 3).to(DEV)
+    m2 = (torch.randn(1, t, generator=g) * 3).to(DEV)  # each group wins some tokens
+    l1 = (torch.rand(1, t, generator=g) * 4 + 1).to(DEV)
+    l2 = (torch.rand(1, t, generator=g) * 4 + 1).to(DEV)
+    return o1, m1, l1, o2, m2, l2
+
+
+@pytest.mark.parametrize("td", [(64, 2048), (33, 777), (128, 512), (7, 63)])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_merge_forward_and_backward(td, dtype):
+    t, d = td
+    print(f"merge {td} {dtype}", flush=True)
+    ins = _merge_inputs(t, d, dtype, seed=t + d)
+    o, m, ell = merge_online_softmax(*ins)
+    ro, rm, rl = c_oracle.merge(*[_np(x)[0] for x in ins])
+    _close(o[0].cpu(), ro, dtype, what="o")
+    _stat_close(m[0].cpu(), rm, "m")
+    _stat_close(ell[0].cpu(), rl, "l")
+
+    leaves = [x.clone().requires_grad_() for x in ins]
+    g = torch.Generator().manual_seed(17)
+    go = torch.randn(1, t, d, generator=g).to(dtype).to(DEV)
+    gm, gl = torch.randn(1, t, generator=g).to(DEV), torch.randn(1, t, generator=g).to(DEV)
+    torch.autograd.backward(merge_online_softmax(*leaves), (go, gm, gl))
+    ref = c_oracle.merge_backward(*[_np(x)[0] for x in ins], _np(go)[0], _np(gm)[0], _np(gl)[0])
+    for leaf, r, name, is_o in zip(leaves, ref, ("do1", "dm1", "dl1", "do2", "dm2", "dl2"),
+                                   (1, 0, 0, 1, 0, 0)):
+        if is_o:
+            _close(leaf.grad[0].cpu(), r, dtype, what=name)
+        else:
+            _stat_close(leaf.grad[0].cpu(), r, name)
+
+
+def test_merge_in_place_and_extreme_separation():
+    """o may alias o1; logits 200 apart stay finite (test_reference.py:153-162)."""
+    ins = list(_merge_inputs(64, 1024, torch.bfloat16, seed=5))
+    ins[4] = ins[1] + 200.0
+    ro, _, rl = c_oracle.merge(*[_np(x)[0] for x in ins])
+    o1 = ins[0].clone()
+    rc = _lib.lib().sy_merge_stats(
+        *[ctypes_ptr(x) for x in (o1, ins[1], ins[2], ins[3], ins[4], ins[5], o1, ins[1], ins[2])],
+        64, 1024, _lib.SY_BF16, _lib.stream_ptr(o1.device))
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert torch.isfinite(o1).all()
+    _close(o1[0].cpu(), ro, torch.bfloat16, what="in-place o")
+
+
+def ctypes_ptr(x):
+    import ctypes
+
+    return ctypes.c_void_p(x.data_ptr())
+
+
+# -- two-phase schedule ------------------------------------------------------
+
+
+@pytest.mark.parametrize("split", [1, 2, 4, 8])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_two_phase_equals_the_single_pass_operator(split, dtype):
+    """test_reference.py:139-150 restated on the GPU: merge then divide equals
+    the single pass, to the dtype's rounding."""
+    v, w = _make(9, 96, 2048, dtype, seed=6)
+    got = block_attn_res_two_phase(v, w, split)
+    oracle = c_oracle.forward(_np(v)[:, 0], _np(w))
+    _close(got[0].cpu(), oracle, dtype, mult=2.5, what="two-phase")
+    single = block_attn_res_triton(v, w)
+    _close(single[0].cpu(), oracle, dtype, what="single pass")
+
+
+def test_two_phase_gradients_match_the_operator():
+    v, w = _make(9, 64, 1024, torch.float32, seed=8)
+    g = torch.randn(1, 64, 1024, generator=torch.Generator().manual_seed(2)).to(DEV)
+    a = v.clone().requires_grad_()
+    wa = w.clone().requires_grad_()
+    block_attn_res_two_phase(a, wa, 4).backward(g)
+    rdv, rdw = c_oracle.backward(_np(v)[:, 0], _np(w), _np(g)[0])
+    _close(a.grad[:, 0].cpu(), rdv, torch.float32, what="dv")
+    _close(wa.grad.cpu(), rdw, torch.float32, what="dw")
+
+
+# -- batched with statistics -------------------------------------------------
+
+
+@pytest.mark.parametrize("nsd", [(9, 8, 2048), (4, 3, 512), (9, 20, 1024), (5, 2, 777)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_batched_with_stats(nsd, dtype):
+    n, s, d = nsd
+    v, _ = _make(n, 64, d, dtype, seed=4)
+    q = (torch.randn(s, d, generator=torch.Generator().manual_seed(1)) * 0.5).to(dtype).to(DEV)
+    with torch.no_grad():
+        o, m, ell = block_attn_res_batched_with_stats(v, q)
+        out = block_attn_res_batched(v, q)
+    for k in range(s):
+        ro, rm, rl = c_oracle.attn_with_stats(_np(v)[:, 0], _np(q)[k])
+        _close(o[k, 0].cpu(), ro, dtype, what=f"o[{k}]")
+        _stat_close(m[k, 0].cpu(), rm, f"m[{k}]")
+        _stat_close(ell[k, 0].cpu(), rl, f"l[{k}]")
+    _close((o.float() / ell.unsqueeze(-1)).to(dtype)[:, 0].cpu(),
+           c_oracle.batched(_np(v)[:, 0], _np(q)), dtype, mult=2.5, what="o/l")
+    assert out.shape == o.shape
+
+
+# -- batched backward --------------------------------------------------------
+
+
+@pytest.mark.parametrize("nstd", [(9, 8, 256, 2048), (4, 3, 128, 512), (9, 1, 64, 4096),
+                                  (2, 8, 100, 1024), (9, 12, 64, 1024), (12, 4, 64, 512),
+                                  (5, 3, 33, 777)])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_batched_backward(nstd, dtype):
+    n, s, t, d = nstd
+    print(f"batched bwd {nstd} {dtype}", flush=True)
+    v, _ = _make(n, t, d, dtype, seed=11)
+    gen = torch.Generator().manual_seed(12)
+    q = (torch.randn(s, d, generator=gen) * 2.0 / d**0.5).to(dtype).to(DEV)
+    g = torch.randn(s, 1, t, d, generator=gen).to(dtype).to(DEV)
+    vv, qq = v.clone().requires_grad_(), q.clone().requires_grad_()
+    out = block_attn_res_batched_train(vv, qq)
+    _close(out[:, 0].cpu(), c_oracle.batched(_np(v)[:, 0], _np(q)), dtype, what="out")
+    out.backward(g)
+    rdv, rdq = c_oracle.batched_backward(_np(v)[:, 0], _np(q), _np(g)[:, 0])
+    _close(vv.grad[:, 0].cpu(), rdv, dtype, what="dv")
+    _close(qq.grad.cpu(), rdq, dtype, what="dq")
+
+
+def test_batched_backward_is_deterministic_and_single_query_consistent():
+    v, w = _make(9, 128, 2048, torch.bfloat16, seed=13)
+    g = torch.randn(1, 1, 128, 2048, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).to(DEV)
+    grads = []
+    for _ in range(2):
+        vv, qq = v.clone().requires_grad_(), w[None].clone().requires_grad_()
+        block_attn_res_batched_train(vv, qq).backward(g)
+        grads.append((vv.grad, qq.grad))
+    assert torch.equal(grads[0][0], grads[1][0]) and torch.equal(grads[0][1], grads[1][1])
+    # S = 1 is the operator: same dv to rounding
+    va, wa = v.clone().requires_grad_(), w.clone().requires_grad_()
+    block_attn_res_triton(va, wa).backward(g[0])
+    rdv, rdw = c_oracle.backward(_np(v)[:, 0], _np(w), _np(g)[0, 0])
+    _close(grads[0][0][:, 0].cpu(), rdv, torch.bfloat16, what="batched dv")
+    _close(grads[0][1][0].cpu(), rdw, torch.bfloat16, what="batched dq")
