@@ -81,6 +81,7 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--title", default="")
     ap.add_argument("--json-out", type=pathlib.Path, default=None)
     ap.add_argument("--sweep", action="store_true")
+    ap.add_argument("--schedule", action="store_true")
     ap.add_argument("--model", action="store_true")
     ap.add_argument("--model-scale", default="1.3B", choices=["1.3B", "small"])
     ap.add_argument("--model-batch", type=int, default=4)
@@ -401,8 +402,13 @@ SWEEP_SHAPES = (
 )
 
 
+DTYPE_TAG = {"bfloat16": "bf16", "float16": "fp16", "float32": "fp32"}
+
+
 def sweep_mode(args):
-    """Configs 3 and 4 of BASELINE.json: one JSON line per shape."""
+    """Configs 3 and 4 of BASELINE.json in ``--dtype``: one JSON line per shape.
+    With --json-out the run is also written as a results file for the
+    regression gate (python -m switchyard.regression)."""
     import torch
 
     from switchyard import _lib, harness
@@ -412,60 +418,229 @@ def sweep_mode(args):
     torch.cuda.set_device(dev)
     lib, st = _lib.lib(), _lib.stream_ptr(dev)
     P = Workload._p
+    dt = getattr(torch, args.dtype)
+    code, tag = _lib.dtype_code(dt), DTYPE_TAG[args.dtype]
+    item = torch.finfo(dt).bits // 8
     gen = torch.Generator(device=dev).manual_seed(0)
+    results = []
     for name, n, b, t, d in SWEEP_SHAPES:
         nt = b * t
-        slab = nt * d * 2
+        slab = nt * d * item
         rot = max(2, min(6, int((3 << 30) // ((2 * n + 3) * slab))))
         sets = []
         for _ in range(rot):
-            v = torch.randn(n, b, t, d, device=dev, generator=gen).to(torch.bfloat16)
-            sets.append(dict(v=v, g=torch.randn(b, t, d, device=dev, generator=gen).to(torch.bfloat16),
-                             out=torch.empty(b, t, d, device=dev, dtype=torch.bfloat16),
+            v = torch.randn(n, b, t, d, device=dev, generator=gen).to(dt)
+            sets.append(dict(v=v, g=torch.randn(b, t, d, device=dev, generator=gen).to(dt),
+                             out=torch.empty(b, t, d, device=dev, dtype=dt),
                              stats=torch.empty(2, n, nt, device=dev), dv=torch.empty_like(v),
-                             dw=torch.empty(d, device=dev, dtype=torch.bfloat16)))
-        w = (0.5 * torch.randn(d, device=dev, generator=gen)).to(torch.bfloat16)
-        ws_bytes = int(lib.sy_bwd_workspace_bytes(n, nt, d, 2, 2))
+                             dw=torch.empty(d, device=dev, dtype=dt)))
+        w = (0.5 * torch.randn(d, device=dev, generator=gen)).to(dt)
+        ws_bytes = int(lib.sy_bwd_workspace_bytes(n, nt, d, code, code))
         ws = torch.empty(max(1, ws_bytes // 4), device=dev)
 
         def fwd(s):
-            _lib.check(lib.sy_fwd(P(s["v"]), P(w), P(s["out"]), P(s["stats"]), n, nt, d, nt * d, 2, 2, 1e-6, st), "sy_fwd")
+            _lib.check(lib.sy_fwd(P(s["v"]), P(w), P(s["out"]), P(s["stats"]), n, nt, d, nt * d, code, code,
+                                  1e-6, st), "sy_fwd")
 
         def bwd(s):
             _lib.check(lib.sy_bwd(P(s["v"]), P(w), P(s["g"]), P(s["stats"]), P(s["dv"]), P(s["dw"]), P(ws),
-                                  ws_bytes, n, nt, d, nt * d, 2, 2, 1e-6, st), "sy_bwd")
+                                  ws_bytes, n, nt, d, nt * d, code, code, 1e-6, st), "sy_bwd")
 
         iters = max(20, min(200, int(2e5 / (n * t * b * d / 1e4))))
         f_ms = harness.time_loop([lambda s=s: fwd(s) for s in sets], device=dev, iters=iters)
         fb_ms = harness.time_loop([lambda s=s: (fwd(s), bwd(s)) for s in sets], device=dev, iters=iters)
-        fb = attn_res_train_bytes(n, b, t, d)
-        fw = attn_res_min_bytes(n, b, t, d)
-        rec = {"sweep": name, "N": n, "B": b, "T": t, "D": d, "dtype": "bf16", "rotating_sets": rot,
+        fb = attn_res_train_bytes(n, b, t, d, item)
+        fw = attn_res_min_bytes(n, b, t, d, item)
+        fplan = _lib.plan(_lib.OP_FWD, n, d, dt)
+        bplan = _lib.plan(_lib.OP_BWD, n, d, dt)
+        rec = {"sweep": name, "impl": "switchyard_hip", "N": n, "B": b, "T": t, "D": d, "dtype": tag,
+               "rotating_sets": rot,
                "fwd_us": round(f_ms * 1e3, 2), "fwd_gbps": round(fw / f_ms / 1e6, 1),
                "fwd_frac_hbm_peak": round(fw / f_ms / 1e6 / HBM_PEAK_GBPS, 4),
                "fwd_bwd_us": round(fb_ms * 1e3, 2), "fwd_bwd_gbps": round(fb / fb_ms / 1e6, 1),
-               "fwd_bwd_frac_hbm_peak": round(fb / fb_ms / 1e6 / HBM_PEAK_GBPS, 4)}
+               "fwd_bwd_frac_hbm_peak": round(fb / fb_ms / 1e6 / HBM_PEAK_GBPS, 4),
+               "workspace_bytes": ws_bytes + 2 * n * nt * 4,
+               "fwd_tile": [fplan["family_name"], fplan["waves_per_token"], fplan["chunks_per_lane"],
+                            fplan["rows_per_tile"]],
+               "bwd_tile": [bplan["family_name"], bplan["waves_per_token"], bplan["chunks_per_lane"],
+                            bplan["rows_per_tile"]]}
         print(json.dumps(rec), flush=True)
+        results.append(rec)
         del sets, ws
         torch.cuda.empty_cache()
     # Config 3: batched, Q=8 queries sharing one read of v.
     n, b, t, d, q = 9, 1, 4096, 2048, 8
     nt = b * t
-    sets = [dict(v=torch.randn(n, b, t, d, device=dev, generator=gen).to(torch.bfloat16),
-                 out=torch.empty(q, b, t, d, device=dev, dtype=torch.bfloat16)) for _ in range(6)]
+    sets = [dict(v=torch.randn(n, b, t, d, device=dev, generator=gen).to(dt),
+                 out=torch.empty(q, b, t, d, device=dev, dtype=dt)) for _ in range(6)]
     gq = torch.Generator().manual_seed(1)
-    queries = (0.5 * torch.randn(q, d, generator=gq)).to(torch.bfloat16).to(dev)
+    queries = (0.5 * torch.randn(q, d, generator=gq)).to(dt).to(dev)
 
     def batched(s):
-        _lib.check(lib.sy_fwd_batched(P(s["v"]), P(queries), P(s["out"]), n, q, nt, d, nt * d, 2, 1e-6, st),
+        _lib.check(lib.sy_fwd_batched(P(s["v"]), P(queries), P(s["out"]), n, q, nt, d, nt * d, code, 1e-6, st),
                    "sy_fwd_batched")
 
     ms = harness.time_loop([lambda s=s: batched(s) for s in sets], device=dev, iters=100)
-    nbytes = attn_res_batched_bytes(n, q, b, t, d)
-    print(json.dumps({"sweep": "batched", "N": n, "B": b, "T": t, "D": d, "Q": q, "dtype": "bf16",
-                      "us": round(ms * 1e3, 2), "gbps": round(nbytes / ms / 1e6, 1),
-                      "frac_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBPS, 4),
-                      "reference_rtx_pro_6000_us": 198.7}), flush=True)
+    nbytes = attn_res_batched_bytes(n, q, b, t, d, item)
+    rec = {"sweep": "batched", "impl": "switchyard_hip", "N": n, "B": b, "T": t, "D": d, "Q": q, "dtype": tag,
+           "fwd_us": round(ms * 1e3, 2), "fwd_gbps": round(nbytes / ms / 1e6, 1),
+           "fwd_frac_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBPS, 4),
+           "reference_rtx_pro_6000_us": 198.7 if tag == "bf16" else None}
+    print(json.dumps(rec), flush=True)
+    results.append(rec)
+    if args.json_out:
+        args.json_out.parent.mkdir(parents=True, exist_ok=True)
+        args.json_out.write_text(json.dumps({"environment": harness.environment(), "dtype": tag,
+                                             "results": results}, indent=1))
+
+
+def schedule_mode(args):
+    """The widened rows at config 2/3 shapes (bf16): pointer-table input vs the
+    stacked operator, attn_with_stats / merge / two-phase, batched statistics,
+    and the batched backward. One JSON line per measurement."""
+    import torch
+
+    from switchyard import _lib, harness
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lib, st = _lib.lib(), _lib.stream_ptr(dev)
+    P = Workload._p
+    dt, code, item = torch.bfloat16, _lib.SY_BF16, 2
+    n, b, t, d, nq = 9, 1, 4096, 2048, 8
+    nt = b * t
+    slab = nt * d * item
+    gen = torch.Generator(device=dev).manual_seed(0)
+    w = (0.5 * torch.randn(d, device=dev, generator=gen)).to(dt)
+    rot = 6
+    results = []
+
+    def emit(name, ms, nbytes, **extra):
+        rec = {"row": name, "N": n, "B": b, "T": t, "D": d, "dtype": "bf16", "us": round(ms * 1e3, 2),
+               "algorithmic_bytes": nbytes, "gbps": round(nbytes / ms / 1e6, 1),
+               "frac_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBPS, 4), **extra}
+        print(json.dumps(rec), flush=True)
+        results.append(rec)
+
+    def timed(fns, iters=100):
+        for f in fns:
+            f()
+        return harness.time_loop(fns, device=dev, iters=iters)
+
+    # --- pointer table vs stacked (config 2) ---------------------------------
+    ws_bytes = int(lib.sy_bwd_workspace_bytes(n, nt, d, code, code))
+    sets = []
+    for _ in range(rot):
+        v = torch.randn(n, b, t, d, device=dev, generator=gen).to(dt)
+        srcs = [torch.randn(b, t, d, device=dev, generator=gen).to(dt) for _ in range(n)]  # separate allocations
+        dvs = [torch.empty(b, t, d, device=dev, dtype=dt) for _ in range(n)]
+        sets.append(dict(v=v, srcs=srcs, tab=_lib.pointer_table(srcs), dvs=dvs, dtab=_lib.pointer_table(dvs),
+                         g=torch.randn(b, t, d, device=dev, generator=gen).to(dt),
+                         out=torch.empty(b, t, d, device=dev, dtype=dt), stats=torch.empty(2, n, nt, device=dev),
+                         dv=torch.empty_like(v), dw=torch.empty(d, device=dev, dtype=dt),
+                         ws=torch.empty(max(1, ws_bytes // 4), device=dev)))
+
+    def fwd_stacked(s):
+        _lib.check(lib.sy_fwd(P(s["v"]), P(w), P(s["out"]), P(s["stats"]), n, nt, d, nt * d, code, code, 1e-6,
+                              st), "sy_fwd")
+
+    def bwd_stacked(s):
+        _lib.check(lib.sy_bwd(P(s["v"]), P(w), P(s["g"]), P(s["stats"]), P(s["dv"]), P(s["dw"]), P(s["ws"]),
+                              ws_bytes, n, nt, d, nt * d, code, code, 1e-6, st), "sy_bwd")
+
+    def fwd_table(s):
+        _lib.check(lib.sy_fwd_table(s["tab"], P(w), P(s["out"]), P(s["stats"]), n, nt, d, code, code, 1e-6, st),
+                   "sy_fwd_table")
+
+    def bwd_table(s):
+        _lib.check(lib.sy_bwd_table(s["tab"], P(w), P(s["g"]), P(s["stats"]), s["dtab"], P(s["dw"]), P(s["ws"]),
+                                    ws_bytes, n, nt, d, code, code, 1e-6, st), "sy_bwd_table")
+
+    def stack_then_fwd(s):  # what a caller with separate sources pays without the table
+        torch.stack(s["srcs"], out=s["v"])
+        fwd_stacked(s)
+
+    fw, fb = (n + 1) * slab, (3 * n + 2) * slab
+    emit("stacked_fwd", timed([lambda s=s: fwd_stacked(s) for s in sets]), fw)
+    emit("table_fwd", timed([lambda s=s: fwd_table(s) for s in sets]), fw)
+    emit("stack_copy_then_fwd", timed([lambda s=s: stack_then_fwd(s) for s in sets]), fw,
+         note="torch.stack of the sources into v, then the stacked forward")
+    emit("stacked_fwd_bwd", timed([lambda s=s: (fwd_stacked(s), bwd_stacked(s)) for s in sets]), fb)
+    emit("table_fwd_bwd", timed([lambda s=s: (fwd_table(s), bwd_table(s)) for s in sets]), fb)
+
+    # --- attn_with_stats, merge, two-phase (config 2) ------------------------
+    for s in sets:
+        s.update(o1=torch.empty(b, t, d, device=dev, dtype=dt), o2=torch.empty(b, t, d, device=dev, dtype=dt),
+                 m1=torch.empty(nt, device=dev), l1=torch.empty(nt, device=dev), m2=torch.empty(nt, device=dev),
+                 l2=torch.empty(nt, device=dev), mo=torch.empty(nt, device=dev), lo=torch.empty(nt, device=dev),
+                 do1=torch.empty(b, t, d, device=dev, dtype=dt), do2=torch.empty(b, t, d, device=dev, dtype=dt),
+                 gm=torch.randn(nt, device=dev, generator=gen), gl=torch.randn(nt, device=dev, generator=gen),
+                 dm1=torch.empty(nt, device=dev), dl1=torch.empty(nt, device=dev),
+                 dm2=torch.empty(nt, device=dev), dl2=torch.empty(nt, device=dev))
+    split = 4
+
+    def stats_fwd(s, lo_, hi_, o, m, ell):
+        v = s["v"][lo_:hi_]
+        _lib.check(lib.sy_attn_with_stats(P(v), P(w), P(o), P(m), P(ell), None, hi_ - lo_, nt, d, nt * d, code,
+                                          code, 1e-6, st), "sy_attn_with_stats")
+
+    def merge(s):
+        _lib.check(lib.sy_merge_stats(P(s["o1"]), P(s["m1"]), P(s["l1"]), P(s["o2"]), P(s["m2"]), P(s["l2"]),
+                                      P(s["out"]), P(s["mo"]), P(s["lo"]), nt, d, code, st), "sy_merge_stats")
+
+    def merge_bwd(s):
+        _lib.check(lib.sy_merge_stats_bwd(P(s["o1"]), P(s["m1"]), P(s["l1"]), P(s["o2"]), P(s["m2"]), P(s["l2"]),
+                                          P(s["g"]), P(s["gm"]), P(s["gl"]), P(s["do1"]), P(s["dm1"]), P(s["dl1"]),
+                                          P(s["do2"]), P(s["dm2"]), P(s["dl2"]), nt, d, code, st),
+                   "sy_merge_stats_bwd")
+
+    emit("attn_with_stats_fwd", timed([lambda s=s: stats_fwd(s, 0, n, s["o1"], s["m1"], s["l1"]) for s in sets]),
+         fw + 2 * nt * 4)
+    for s in sets:
+        stats_fwd(s, 0, split, s["o1"], s["m1"], s["l1"])
+        stats_fwd(s, split, n, s["o2"], s["m2"], s["l2"])
+    emit("merge_fwd", timed([lambda s=s: merge(s) for s in sets]), 3 * slab + 6 * nt * 4)
+    emit("merge_bwd", timed([lambda s=s: merge_bwd(s) for s in sets]), 5 * slab + 10 * nt * 4)
+    emit("two_phase_fwd", timed([lambda s=s: (stats_fwd(s, 0, split, s["o1"], s["m1"], s["l1"]),
+                                              stats_fwd(s, split, n, s["o2"], s["m2"], s["l2"]), merge(s))
+                                 for s in sets]), fw,
+         note=f"groups [0,{split}) and [{split},{n}) then the merge; bytes counted as the single pass's")
+    del sets
+    torch.cuda.empty_cache()
+
+    # --- batched with statistics and batched backward (config 3) ------------
+    q = (0.5 * torch.randn(nq, d, generator=torch.Generator().manual_seed(1))).to(dt).to(dev)
+    bw_bytes = int(lib.sy_bwd_batched_workspace_bytes(n, nq, nt, d, code))
+    sets = []
+    for _ in range(rot):
+        v = torch.randn(n, b, t, d, device=dev, generator=gen).to(dt)
+        sets.append(dict(v=v, g=torch.randn(nq, b, t, d, device=dev, generator=gen).to(dt),
+                         o=torch.empty(nq, b, t, d, device=dev, dtype=dt), m=torch.empty(nq, nt, device=dev),
+                         ell=torch.empty(nq, nt, device=dev), dv=torch.empty_like(v),
+                         dq=torch.empty(nq, d, device=dev, dtype=dt), ws=torch.empty(max(1, bw_bytes // 4), device=dev)))
+
+    def batched_fwd(s):
+        _lib.check(lib.sy_fwd_batched(P(s["v"]), P(q), P(s["o"]), n, nq, nt, d, nt * d, code, 1e-6, st),
+                   "sy_fwd_batched")
+
+    def batched_stats(s):
+        _lib.check(lib.sy_batched_with_stats(P(s["v"]), P(q), P(s["o"]), P(s["m"]), P(s["ell"]), n, nq, nt, d,
+                                             nt * d, code, 1e-6, st), "sy_batched_with_stats")
+
+    def batched_bwd(s):
+        _lib.check(lib.sy_bwd_batched(P(s["v"]), P(q), P(s["g"]), P(s["dv"]), P(s["dq"]), P(s["ws"]), bw_bytes, n,
+                                      nq, nt, d, nt * d, code, 1e-6, st), "sy_bwd_batched")
+
+    bf = (n + nq) * slab + nq * d * item
+    emit("batched_fwd", timed([lambda s=s: batched_fwd(s) for s in sets]), bf, Q=nq)
+    emit("batched_with_stats_fwd", timed([lambda s=s: batched_stats(s) for s in sets]), bf + 2 * nq * nt * 4, Q=nq)
+    emit("batched_bwd", timed([lambda s=s: batched_bwd(s) for s in sets]), (2 * n + nq) * slab + 2 * nq * d * item,
+         Q=nq, workspace_bytes=bw_bytes,
+         note="reads v and the Q output gradients once, writes dv once; S separate backward calls would move "
+              f"{nq * (2 * n + 1)} slabs instead of {2 * n + nq}")
+    if args.json_out:
+        args.json_out.parent.mkdir(parents=True, exist_ok=True)
+        args.json_out.write_text(json.dumps({"environment": harness.environment(), "results": results}, indent=1))
 
 
 MODEL_SCALES = {
@@ -531,6 +706,9 @@ def main() -> None:
     args = parse_args()
     if args.sweep:
         sweep_mode(args)
+        return
+    if args.schedule:
+        schedule_mode(args)
         return
     if args.model:
         model_mode(args)

@@ -27,23 +27,26 @@ int status(hipError_t e) { return e == hipSuccess ? SY_OK : (int)e; }
 std::mutex g_mu;
 std::map<int, int> g_cus;                                   // device -> CU count
 
-hipError_t bwd_resources(const sy_plan& p, int dtype, bool stats, KernelRes* out) {
-  if (dtype == SY_BF16) return bwd_vec_resources_bf16(p, stats, out);
-  if (dtype == SY_F16) return bwd_vec_resources_f16(p, stats, out);
-  return bwd_vec_resources_f32(p, stats, out);
+// variant: 0 operator over stacked rows, 1 over per-row pointers, 2 the
+// (o, m, l) gradient over stacked rows (BwdVariant in sy_kernels.hpp).
+hipError_t bwd_resources(const sy_plan& p, int dtype, bool stats, int variant, KernelRes* out) {
+  if (dtype == SY_BF16) return bwd_vec_resources_bf16(p, stats, variant, out);
+  if (dtype == SY_F16) return bwd_vec_resources_f16(p, stats, variant, out);
+  return bwd_vec_resources_f32(p, stats, variant, out);
 }
 
 // Persistent workgroup count of the backward: every CU filled at the
 // kernel's register/LDS occupancy, never more than there are token slots.
-// Deterministic in (plan, n_tok, stats, device), which keeps dw bit-stable.
-int bwd_grid(const sy_plan& p, int64_t n_tok, int dtype, bool stats, int* grid) {
+// Deterministic in (plan, n_tok, stats, addressing, device), which keeps dw
+// bit-stable.
+int bwd_grid(const sy_plan& p, int64_t n_tok, int dtype, bool stats, int variant, int* grid) {
   int cus = 0;
   hipError_t e = cu_count(&cus);
   if (e != hipSuccess) return e == hipErrorNoDevice ? SY_ERR_DEVICE : (int)e;
   int per_cu = 4;
   if (p.family != SY_FAMILY_GENERIC) {
     KernelRes r;
-    e = bwd_resources(p, dtype, stats, &r);
+    e = bwd_resources(p, dtype, stats, variant, &r);
     if (e != hipSuccess) return (int)e;
     per_cu = r.blocks_per_cu;
   }
@@ -195,7 +198,7 @@ int fwd_impl(const RowTable& v, bool v_ok, const void* w, void* out, float* stat
 // Main backward kernel over row tables: dv and the fp32 dw partials.
 // *rows_out receives the partial row count (the persistent grid).
 int bwd_main_impl(const RowTable& v, bool v_ok, const void* w, const void* g, const float* stats,
-                  const float* gm, const float* gl, const RowTable& dv, bool dv_ok,
+                  const float* gm, const float* gl, const RowTable& dv, bool dv_ok, bool listed,
                   void* workspace, int64_t workspace_bytes, int64_t n_src, int64_t n_tok,
                   int64_t d, int v_dtype, int w_dtype, float eps, hipStream_t s, int* rows_out) {
   *rows_out = 0;
@@ -206,11 +209,12 @@ int bwd_main_impl(const RowTable& v, bool v_ok, const void* w, const void* g, co
   if (rc != SY_OK) return rc;
   apply_tile_override(SY_OP_BWD, n_src, d, &p);
   int grid = 0;
-  rc = bwd_grid(p, n_tok, v_dtype, stats != nullptr, &grid);
+  const int variant = listed ? 1 : (gm != nullptr ? 2 : 0);
+  rc = bwd_grid(p, n_tok, v_dtype, stats != nullptr, variant, &grid);
   if (rc != SY_OK) return rc;
   if (workspace == nullptr || workspace_bytes < (int64_t)grid * d * (int64_t)sizeof(float))
     return SY_ERR_WORKSPACE;
-  const BwdArgs a{v,  w,          g,     stats,  gm,      gl,      dv,  (float*)workspace,
+  const BwdArgs a{v,      w,       g,     stats,  gm,      gl,      dv,  (float*)workspace, listed,
                   (int)n_src, n_tok, (int)d, v_dtype, w_dtype, eps};
   const hipError_t e =
       p.family == SY_FAMILY_GENERIC ? launch_bwd_generic(a, grid, s) : bwd_vec(p, a, grid, s);
@@ -222,12 +226,12 @@ int bwd_main_impl(const RowTable& v, bool v_ok, const void* w, const void* g, co
 // Main kernel then the fixed-order dw reduction (dw is written even with no
 // tokens: it is then zero).
 int bwd_impl(const RowTable& v, bool v_ok, const void* w, const void* g, const float* stats,
-             const float* gm, const float* gl, const RowTable& dv, bool dv_ok, void* dw,
+             const float* gm, const float* gl, const RowTable& dv, bool dv_ok, bool listed, void* dw,
              void* workspace, int64_t workspace_bytes, int64_t n_src, int64_t n_tok, int64_t d,
              int v_dtype, int w_dtype, float eps, hipStream_t s) {
   int rows = 0;
-  const int rc = bwd_main_impl(v, v_ok, w, g, stats, gm, gl, dv, dv_ok, workspace, workspace_bytes,
-                               n_src, n_tok, d, v_dtype, w_dtype, eps, s, &rows);
+  const int rc = bwd_main_impl(v, v_ok, w, g, stats, gm, gl, dv, dv_ok, listed, workspace,
+                               workspace_bytes, n_src, n_tok, d, v_dtype, w_dtype, eps, s, &rows);
   if (rc != SY_OK) return rc;
   return status(launch_dw_reduce((const float*)workspace, rows, (int)d, dw, w_dtype, s));
 }
@@ -358,10 +362,12 @@ int64_t sy_bwd_workspace_bytes(int64_t n_src, int64_t n_tok, int64_t d, int v_dt
   int64_t g = 0;
   for (const sy_plan* pp : {&pv, &pg}) {
     for (bool st : {true, false}) {
-      int gi = 0;
-      rc = bwd_grid(*pp, n_tok, v_dtype, st, &gi);
-      if (rc != SY_OK) return rc;
-      if (gi > g) g = gi;
+      for (int var : {0, 1, 2}) {
+        int gi = 0;
+        rc = bwd_grid(*pp, n_tok, v_dtype, st, var, &gi);
+        if (rc != SY_OK) return rc;
+        if (gi > g) g = gi;
+      }
     }
   }
   return g * d * (int64_t)sizeof(float);
@@ -378,7 +384,7 @@ int sy_bwd(const void* v, const void* w, const void* grad_out, const float* stat
   bool vok = false, dok = false;
   const RowTable tv = stacked(v, n_src, src_stride, v_dtype, &vok);
   const RowTable td = stacked(dv, n_src, n_tok * d, v_dtype, &dok);
-  return bwd_impl(tv, vok, w, grad_out, stats, nullptr, nullptr, td, dok, dw, workspace,
+  return bwd_impl(tv, vok, w, grad_out, stats, nullptr, nullptr, td, dok, false, dw, workspace,
                   workspace_bytes, n_src, n_tok, d, v_dtype, w_dtype, eps, (hipStream_t)stream);
 }
 
@@ -398,7 +404,7 @@ int sy_bwd_table(const void* const* v_rows, const void* w, const void* grad_out,
   if (rc != SY_OK) return rc;
   rc = listed(reinterpret_cast<const void* const*>(dv_rows), n_src, n_tok, &td, &dok);
   if (rc != SY_OK) return rc;
-  return bwd_impl(tv, vok, w, grad_out, stats, nullptr, nullptr, td, dok, dw, workspace,
+  return bwd_impl(tv, vok, w, grad_out, stats, nullptr, nullptr, td, dok, true, dw, workspace,
                   workspace_bytes, n_src, n_tok, d, v_dtype, w_dtype, eps, (hipStream_t)stream);
 }
 
@@ -416,7 +422,7 @@ int sy_attn_with_stats_bwd(const void* v, const void* w, const void* grad_o, con
   bool vok = false, dok = false;
   const RowTable tv = stacked(v, n_src, src_stride, v_dtype, &vok);
   const RowTable td = stacked(dv, n_src, n_tok * d, v_dtype, &dok);
-  return bwd_impl(tv, vok, w, grad_o, stats, grad_m, grad_l, td, dok, dw, workspace,
+  return bwd_impl(tv, vok, w, grad_o, stats, grad_m, grad_l, td, dok, false, dw, workspace,
                   workspace_bytes, n_src, n_tok, d, v_dtype, w_dtype, eps, (hipStream_t)stream);
 }
 
@@ -431,7 +437,7 @@ int sy_bwd_main(const void* v, const void* w, const void* grad_out, const float*
   const RowTable tv = stacked(v, n_src, src_stride, v_dtype, &vok);
   const RowTable td = stacked(dv, n_src, n_tok * d, v_dtype, &dok);
   int rows = 0;
-  return bwd_main_impl(tv, vok, w, grad_out, stats, nullptr, nullptr, td, dok, workspace,
+  return bwd_main_impl(tv, vok, w, grad_out, stats, nullptr, nullptr, td, dok, false, workspace,
                        workspace_bytes, n_src, n_tok, d, v_dtype, w_dtype, eps,
                        (hipStream_t)stream, &rows);
 }
@@ -446,7 +452,7 @@ int64_t sy_bwd_partial_rows(int64_t n_src, int64_t n_tok, int64_t d, int v_dtype
   if (rc != SY_OK) return rc;
   apply_tile_override(SY_OP_BWD, n_src, d, &p);
   int grid = 0;
-  rc = bwd_grid(p, n_tok, v_dtype, has_stats != 0, &grid);
+  rc = bwd_grid(p, n_tok, v_dtype, has_stats != 0, 0, &grid);
   return rc != SY_OK ? rc : grid;
 }
 
@@ -471,9 +477,9 @@ int sy_kernel_info(int op, int64_t n_src, int64_t n_tok, int64_t d, int v_dtype,
         : v_dtype == SY_F16 ? launch_fwd_vec_f16(p, a, nullptr, &r)
                             : launch_fwd_vec_f32(p, a, nullptr, &r);
   } else {
-    e = bwd_resources(p, v_dtype, true, &r);
+    e = bwd_resources(p, v_dtype, true, 0, &r);
     if (e == hipSuccess) {
-      rc = bwd_grid(p, n_tok, v_dtype, true, &r.grid);
+      rc = bwd_grid(p, n_tok, v_dtype, true, 0, &r.grid);
       if (rc != SY_OK) return rc;
     }
   }

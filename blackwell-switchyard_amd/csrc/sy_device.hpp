@@ -43,6 +43,19 @@ __host__ __device__ __forceinline__ S* row_of(const RowTable& t, int n) {
                         : reinterpret_cast<S*>(static_cast<char*>(t.p[0]) + (int64_t)n * t.stride_bytes);
 }
 
+// Row n with the addressing mode fixed at compile time: LISTED reads p[n]
+// (n < kTableRows), otherwise p[0] + n*stride_bytes. Kernels that are short of
+// SGPRs use this: the stacked form keeps one pointer and a stride live, where
+// per-row pointers would take two SGPRs per row.
+template <bool LISTED, class S>
+__device__ __forceinline__ S* row_at(const RowTable& t, int n) {
+  if constexpr (LISTED) {
+    return static_cast<S*>(t.p[n]);
+  } else {
+    return reinterpret_cast<S*>(static_cast<char*>(t.p[0]) + (int64_t)n * t.stride_bytes);
+  }
+}
+
 // Buffer resource word 3 for gfx9-family raw buffers (32-bit dword format).
 constexpr int kRsrcFlags = 0x00020000;
 

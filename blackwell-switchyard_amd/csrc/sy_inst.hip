@@ -125,14 +125,21 @@ hipError_t SY_FN(launch_batched_vec_)(const sy_plan& p, const BatchedArgs& a, hi
 
 // The backward's grid must be known before launch (it sizes the workspace),
 // so it is computed here from the instantiation's resources.
-hipError_t SY_FN(bwd_vec_resources_)(const sy_plan& p, bool stats, KernelRes* out) {
-#define X(W_, V_, N_)                                                                 \
-  if (tile_is(p, W_, V_, N_)) {                                                       \
-    constexpr int kB = BwdGeom<W_>::kBlock;                                           \
-    static const KernelRes with = resources_of(k_bwd<T, W_, V_, N_, true>, kB);       \
-    static const KernelRes without = resources_of(k_bwd<T, W_, V_, N_, false>, kB);   \
-    *out = stats ? with : without;                                                    \
-    return hipSuccess;                                                                \
+// variant: a BwdVariant (kBwdStacked, kBwdListed, kBwdStatsGrad).
+hipError_t SY_FN(bwd_vec_resources_)(const sy_plan& p, bool stats, int variant, KernelRes* out) {
+  if (variant < 0 || variant > 2) return hipErrorInvalidValue;
+#define X(W_, V_, N_)                                                                        \
+  if (tile_is(p, W_, V_, N_)) {                                                              \
+    constexpr int kB = BwdGeom<W_>::kBlock;                                                  \
+    static const KernelRes r[2][3] = {                                                       \
+        {resources_of(k_bwd<T, W_, V_, N_, false, kBwdStacked>, kB),                         \
+         resources_of(k_bwd<T, W_, V_, N_, false, kBwdListed>, kB),                          \
+         resources_of(k_bwd<T, W_, V_, N_, false, kBwdStatsGrad>, kB)},                      \
+        {resources_of(k_bwd<T, W_, V_, N_, true, kBwdStacked>, kB),                          \
+         resources_of(k_bwd<T, W_, V_, N_, true, kBwdListed>, kB),                           \
+         resources_of(k_bwd<T, W_, V_, N_, true, kBwdStatsGrad>, kB)}};                      \
+    *out = r[stats ? 1 : 0][variant];                                                        \
+    return hipSuccess;                                                                       \
   }
   SY_TILES(X)
 #undef X
@@ -143,22 +150,27 @@ hipError_t SY_FN(launch_bwd_vec_)(const sy_plan& p, const BwdArgs& a, int grid, 
   const float inv_d = 1.0f / (float)a.d;
   const int64_t slots = (int64_t)grid * p.tokens_per_block;
   const int n_iter = (int)cdiv(a.n_tok, slots);
+#define SY_BWD_LAUNCH(W_, V_, N_, ST_, LI_)                                                  \
+  hipLaunchKernelGGL((k_bwd<T, W_, V_, N_, ST_, LI_>), dim3(grid), dim3(BwdGeom<W_>::kBlock), 0, \
+                     s, a.v, (const St*)a.w, (const St*)a.g, a.stats, a.gm, a.gl, a.dv, a.partial, \
+                     a.n_src, a.n_tok, a.d, a.eps, inv_d, n_iter)
 #define X(W_, V_, N_)                                                                        \
   if (tile_is(p, W_, V_, N_)) {                                                              \
-    constexpr int kB = BwdGeom<W_>::kBlock;                                                  \
+    const int var = a.listed ? kBwdListed : (a.gm != nullptr ? kBwdStatsGrad : kBwdStacked);  \
     if (a.stats != nullptr) {                                                                \
-      hipLaunchKernelGGL((k_bwd<T, W_, V_, N_, true>), dim3(grid), dim3(kB), 0, s, a.v,      \
-                         (const St*)a.w, (const St*)a.g, a.stats, a.gm, a.gl, a.dv,          \
-                         a.partial, a.n_src, a.n_tok, a.d, a.eps, inv_d, n_iter);            \
+      if (var == kBwdListed) SY_BWD_LAUNCH(W_, V_, N_, true, kBwdListed);                    \
+      else if (var == kBwdStatsGrad) SY_BWD_LAUNCH(W_, V_, N_, true, kBwdStatsGrad);         \
+      else SY_BWD_LAUNCH(W_, V_, N_, true, kBwdStacked);                                     \
     } else {                                                                                 \
-      hipLaunchKernelGGL((k_bwd<T, W_, V_, N_, false>), dim3(grid), dim3(kB), 0, s, a.v,     \
-                         (const St*)a.w, (const St*)a.g, a.stats, a.gm, a.gl, a.dv,          \
-                         a.partial, a.n_src, a.n_tok, a.d, a.eps, inv_d, n_iter);            \
+      if (var == kBwdListed) SY_BWD_LAUNCH(W_, V_, N_, false, kBwdListed);                   \
+      else if (var == kBwdStatsGrad) SY_BWD_LAUNCH(W_, V_, N_, false, kBwdStatsGrad);        \
+      else SY_BWD_LAUNCH(W_, V_, N_, false, kBwdStacked);                                    \
     }                                                                                        \
     return hipGetLastError();                                                                \
   }
   SY_TILES(X)
 #undef X
+#undef SY_BWD_LAUNCH
   return hipErrorInvalidConfiguration;
 }
 

@@ -575,18 +575,28 @@ k_sol_res(const RowTable v, typename T::storage* __restrict__ out, int n_src, in
 //     dlogit_n = p_n (G_n + gl)                              n != k
 //     dlogit_k = gm - sum_{n != k} p_n (G_n + gl)           (p_k = 1, m = logit_k)
 // and dv_n = p_n g + da_n w + c_n v_n with da_n, c_n as above.
+// VAR (a BwdVariant) fixes at compile time what the kernel is: the operator's
+// gradient over stacked rows (base + n*stride), the same over per-row pointers
+// for v and dv (the pointer-list entry points), or the (o, m, l) gradient over
+// stacked rows. Each variant keeps only its own scalar code and addressing:
+// per-row pointers cost two SGPRs a row and the (o, m, l) algebra extra VALU,
+// which the operator's kernel does not pay.
 // grad_out and each source row are refilled with the next token's data as soon
 // as they have been consumed.
 // dw: each slot accumulates in registers; at the end the slots are folded in
 // a fixed tree through LDS and the workgroup writes one fp32 row of `partial`.
 // No float atomics anywhere, so dw is bit-reproducible for a given grid.
-template <class T, int W, int VPL, int NR, bool STATS>
+enum BwdVariant { kBwdStacked = 0, kBwdListed = 1, kBwdStatsGrad = 2 };
+
+template <class T, int W, int VPL, int NR, bool STATS, int VAR>
 __global__ void __launch_bounds__(BwdGeom<W>::kBlock)
 k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
       const typename T::storage* __restrict__ g, const float* __restrict__ stats,
       const float* __restrict__ gm, const float* __restrict__ gl, const RowTable dv,
       float* __restrict__ partial, int n_src, int64_t n_tok, int d, float eps, float inv_d,
       int n_iter) {
+  constexpr bool LISTED = VAR == kBwdListed;
+  constexpr bool GRAD_STATS = VAR == kBwdStatsGrad;
   using S = typename T::storage;
   constexpr int CE = T::ce;
   constexpr int TPB = BwdGeom<W>::kTpb;
@@ -640,7 +650,7 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
 #pragma unroll
     for (int n = 0; n < NR; ++n) {
       if (n < rows) {
-        const auto r = make_rsrc(row_of<const S>(v, n) + t0 * d, row_bytes);
+        const auto r = make_rsrc(row_at<LISTED, const S>(v, n) + t0 * d, row_bytes);
 #pragma unroll
         for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
       }
@@ -688,7 +698,7 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
     // its tiny dlogit to full relative precision instead of G_max - S ~ 0.
     float lg[NR], rr[NR];
     float m = -INFINITY, gref = 0.0f;
-    int top = 0;
+    [[maybe_unused]] int top = 0;
 #pragma unroll
     for (int n = 0; n < NR; ++n) {
       if (n < rows) {
@@ -702,7 +712,7 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
         if (lg[n] > m) {
           m = lg[n];
           gref = part[n];
-          top = n;
+          if constexpr (GRAD_STATS) top = n;
         }
       }
     }
@@ -716,7 +726,7 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
       }
     // Afterwards dlogit_n = al[n] * (part[n] - sdev) in both modes.
     float sdev = 0.0f;
-    if (gm == nullptr) {
+    if constexpr (!GRAD_STATS) {
       const float inv_l = 1.0f / l;
 #pragma unroll
       for (int n = 0; n < NR; ++n)
@@ -757,7 +767,7 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
         const float da = dlogit * rr[n];
         const float c = -dlogit * lg[n] * rr[n] * rr[n] * inv_d;
         const float da_w = da * dw_on;
-        const auto dr = make_rsrc(row_of<S>(dv, n) + tok * d, live ? row_bytes : 0u);
+        const auto dr = make_rsrc(row_at<LISTED, S>(dv, n) + tok * d, live ? row_bytes : 0u);
 #pragma unroll
         for (int j = 0; j < VPL; ++j) {
           float f[CE];
@@ -770,7 +780,7 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
           st16_stream(dr, lane_off + j * kStep, pack<T>(f));
         }
         if (more) {
-          const auto r = make_rsrc(row_of<const S>(v, n) + nxt * d, row_bytes);
+          const auto r = make_rsrc(row_at<LISTED, const S>(v, n) + nxt * d, row_bytes);
 #pragma unroll
           for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
         }
@@ -869,7 +879,7 @@ k_bwd_batched(const RowTable v, const typename T::storage* __restrict__ q,
     const int64_t t0 = first < n_tok ? first : n_tok - 1;
 #pragma unroll
     for (int n = 0; n < NR; ++n)
-      if (n < rows) x[n] = ld16_stream(make_rsrc(row_of<const S>(v, n) + t0 * d, row_bytes), lane_off);
+      if (n < rows) x[n] = ld16_stream(make_rsrc(row_at<false, const S>(v, n) + t0 * d, row_bytes), lane_off);
   }
 
   [[maybe_unused]] int phase = 0;
@@ -989,8 +999,8 @@ k_bwd_batched(const RowTable v, const typename T::storage* __restrict__ q,
         float f[CE];
 #pragma unroll
         for (int e = 0; e < CE; ++e) f[e] = fmaf(cacc[n], elem<T>(x[n], e), dva[n][e]);
-        st16_stream(make_rsrc(row_of<S>(dv, n) + tok * d, live ? row_bytes : 0u), lane_off, pack<T>(f));
-        if (more) x[n] = ld16_stream(make_rsrc(row_of<const S>(v, n) + nxt * d, row_bytes), lane_off);
+        st16_stream(make_rsrc(row_at<false, S>(dv, n) + tok * d, live ? row_bytes : 0u), lane_off, pack<T>(f));
+        if (more) x[n] = ld16_stream(make_rsrc(row_at<false, const S>(v, n) + nxt * d, row_bytes), lane_off);
       }
     }
   }

@@ -62,6 +62,7 @@ struct BwdArgs {
   const float* gl;  // dL/dl [n_tok]
   RowTable dv;
   float* partial;   // [grid][d] fp32
+  bool listed;      // v and dv rows from per-row pointers (else stacked; gm must be null)
   int n_src;
   int64_t n_tok;
   int d;
@@ -128,7 +129,7 @@ struct KernelRes {
   hipError_t launch_sol_vec_##NAME(const sy_plan& p, const FwdArgs& a, hipStream_t s);         \
   hipError_t launch_batched_vec_##NAME(const sy_plan& p, const BatchedArgs& a, hipStream_t s); \
   hipError_t launch_bwd_vec_##NAME(const sy_plan& p, const BwdArgs& a, int grid, hipStream_t s); \
-  hipError_t bwd_vec_resources_##NAME(const sy_plan& p, bool stats, KernelRes* out);          \
+  hipError_t bwd_vec_resources_##NAME(const sy_plan& p, bool stats, int variant, KernelRes* out); \
   hipError_t launch_bwd_batched_vec_##NAME(const sy_plan& p, const BwdBatchedArgs& a, int grid, \
                                            hipStream_t s);                                    \
   hipError_t bwd_batched_vec_resources_##NAME(const sy_plan& p, KernelRes* out);
