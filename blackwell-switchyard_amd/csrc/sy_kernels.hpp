@@ -29,12 +29,12 @@ struct FwdGeom {
   static constexpr int kTpb = kBlock / (64 * W);
 };
 
-// Backward: persistent 512-thread workgroups (two waves per SIMD at most
-// 256 VGPRs each); kTpb token slots run side by side.
+// Backward: persistent workgroups of bwd_block(W) threads (512: two waves per
+// SIMD at most 256 VGPRs each); kTpb token slots run side by side.
 template <int W>
 struct BwdGeom {
-  static constexpr int kBlock = 512;
-  static constexpr int kTpb = 512 / (64 * W);
+  static constexpr int kBlock = bwd_block(W);
+  static constexpr int kTpb = kBlock / (64 * W);
 };
 
 // Sum wave-uniform per-row values across the W waves of each token slot.

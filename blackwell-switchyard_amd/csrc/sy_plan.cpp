@@ -56,8 +56,8 @@ void set(sy_plan* p, int family, int w, int vpl, int nr, int ce, int op, int64_t
     return;
   }
   if (op == SY_OP_BWD) {
-    p->block_threads = 512;
-    p->tokens_per_block = 512 / (64 * w);
+    p->block_threads = bwd_block(w);
+    p->tokens_per_block = p->block_threads / (64 * w);
   } else {
     p->block_threads = 64 * w > 256 ? 64 * w : 256;
     p->tokens_per_block = p->block_threads / (64 * w);
