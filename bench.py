@@ -230,20 +230,31 @@ def cpu_baseline_leg(wl, args, torch):
     # -- checker: GPU op on a token slice vs float64 oracle -------------------
     ts = min(512, wl.t)
     vs, gs = v[:, :, :ts].contiguous(), g[:, :ts].contiguous()
-    vt = vs.to(wl.dev).requires_grad_(True)
-    wt = w.to(wl.dev).requires_grad_(True)
-    out = block_attn_res_hip(vt, wt)
-    out.backward(gs.to(wl.dev))
-    o64 = oref.block_attn_res_oracle(vs, w)
-    dv64, dw64 = oref.oracle_grads(vs, w, gs)
-    check = {}
-    for name, got, ref in (("out", out, o64), ("dv", vt.grad, dv64), ("dw", wt.grad, dw64)):
-        err, floor = oref.rel_l2(got, ref), oref.dtype_floor(ref, wl.dtype)
-        check[name] = {"rel_l2": err, "floor": floor, "ratio": err / floor if floor else None}
+
+    def ratios(wq):
+        vt = vs.to(wl.dev).requires_grad_(True)
+        wt = wq.to(wl.dev).requires_grad_(True)
+        out = block_attn_res_hip(vt, wt)
+        out.backward(gs.to(wl.dev))
+        o64 = oref.block_attn_res_oracle(vs, wq)
+        dv64, dw64 = oref.oracle_grads(vs, wq, gs)
+        res = {}
+        for name, got, ref in (("out", out, o64), ("dv", vt.grad, dv64), ("dw", wt.grad, dw64)):
+            err, floor = oref.rel_l2(got, ref), oref.dtype_floor(ref, wl.dtype)
+            res[name] = {"rel_l2": err, "floor": floor, "ratio": err / floor if floor else None}
+        return res, out
+
+    check, out = ratios(w)
     # Token independence: the slice's output equals the full run's first tokens.
     full = wl.sets[0]["out"][:, :ts].cpu()
     check["slice_matches_full_run"] = bool(torch.equal(out.detach().cpu(), full))
-    check["ok"] = all(check[k]["ratio"] is not None and check[k]["ratio"] <= 1.10 for k in ("out", "dv", "dw"))
+    # The reference's own regime (bench/bench_operator.py:326-336): w = randn(D)
+    # scaled to ||w|| = 1, logits of order one. Timing does not depend on w.
+    wu = torch.randn(wl.d, generator=torch.Generator().manual_seed(1))
+    unit, _ = ratios((wu / wu.norm()).to(wl.dtype))
+    check["unit_norm_query"] = unit
+    check["ok"] = all(r[k]["ratio"] is not None and r[k]["ratio"] <= 1.10
+                      for r in (check, unit) for k in ("out", "dv", "dw"))
 
     # -- timed CPU baseline ---------------------------------------------------
     threads = torch.get_num_threads()

@@ -57,12 +57,17 @@ __device__ __forceinline__ S* row_at(const RowTable& t, int n) {
 }
 
 // Threads per backward workgroup (token slots x waves per token), at least one
-// token's waves. A build-time constant (-DSY_BWD_BLOCK=...) so that kernels and
-// the host plan agree; 512 measured best on MI355X (128: +9%, 256: equal).
+// token's waves. Two- and one-chunk tiles use SY_BWD_BLOCK (512 measured best on
+// MI355X: 128 +9%, 256 equal), i.e. two waves per SIMD at <= 256 VGPRs. Four-chunk
+// tiles use 256 threads: one wave per SIMD, so a wave may hold 512 registers
+// (256 VGPRs + 256 AGPRs) -- the 144-register tile plus everything else, with
+// no spills. A build-time constant so that kernels and the host plan agree.
 #ifndef SY_BWD_BLOCK
 #define SY_BWD_BLOCK 512
 #endif
-constexpr int bwd_block(int w) { return SY_BWD_BLOCK > 64 * w ? SY_BWD_BLOCK : 64 * w; }
+constexpr int bwd_block(int w, int vpl) {
+  return (vpl >= 4 ? 256 : SY_BWD_BLOCK) > 64 * w ? (vpl >= 4 ? 256 : SY_BWD_BLOCK) : 64 * w;
+}
 
 // Buffer resource word 3 for gfx9-family raw buffers (32-bit dword format).
 constexpr int kRsrcFlags = 0x00020000;

@@ -130,7 +130,7 @@ hipError_t SY_FN(bwd_vec_resources_)(const sy_plan& p, bool stats, int variant, 
   if (variant < 0 || variant > 2) return hipErrorInvalidValue;
 #define X(W_, V_, N_)                                                                        \
   if (tile_is(p, W_, V_, N_)) {                                                              \
-    constexpr int kB = BwdGeom<W_>::kBlock;                                                  \
+    constexpr int kB = BwdGeom<W_, V_>::kBlock;                                              \
     static const KernelRes r[2][3] = {                                                       \
         {resources_of(k_bwd<T, W_, V_, N_, false, kBwdStacked>, kB),                         \
          resources_of(k_bwd<T, W_, V_, N_, false, kBwdListed>, kB),                          \
@@ -151,7 +151,7 @@ hipError_t SY_FN(launch_bwd_vec_)(const sy_plan& p, const BwdArgs& a, int grid, 
   const int64_t slots = (int64_t)grid * p.tokens_per_block;
   const int n_iter = (int)cdiv(a.n_tok, slots);
 #define SY_BWD_LAUNCH(W_, V_, N_, ST_, LI_)                                                  \
-  hipLaunchKernelGGL((k_bwd<T, W_, V_, N_, ST_, LI_>), dim3(grid), dim3(BwdGeom<W_>::kBlock), 0, \
+  hipLaunchKernelGGL((k_bwd<T, W_, V_, N_, ST_, LI_>), dim3(grid), dim3(BwdGeom<W_, V_>::kBlock), 0, \
                      s, a.v, (const St*)a.w, (const St*)a.g, a.stats, a.gm, a.gl, a.dv, a.partial, \
                      a.n_src, a.n_tok, a.d, a.eps, inv_d, n_iter)
 #define X(W_, V_, N_)                                                                        \

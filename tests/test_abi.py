@@ -216,14 +216,25 @@ def test_batched_query_cap():
     assert plan(_lib.OP_BATCHED, 9, 2048, n_q=17)["family_name"] == "per_query"
 
 
-def test_backward_never_takes_a_four_chunk_tile():
-    for n in (1, 2, 4, 9):
-        for d in (512, 1024, 2048, 4096, 8192):
-            p = plan(_lib.OP_BWD, n, d)
-            if p["family_name"] == "resident":
-                assert p["chunks_per_lane"] <= 2
-                assert p["block_threads"] == 512
-                assert p["tokens_per_block"] * p["waves_per_token"] == 8
+def test_backward_takes_four_chunks_only_with_one_wave_per_token():
+    """Four chunks per lane run one wave per SIMD (256-thread workgroups, 512
+    registers); every other backward tile runs two waves per SIMD (512 threads)."""
+    for n in (1, 2, 4, 9, 16):
+        for d in (512, 1024, 1536, 2048, 4096, 8192):
+            for dt in (torch.bfloat16, torch.float32):
+                p = plan(_lib.OP_BWD, n, d, dt)
+                if p["family_name"] != "resident":
+                    continue
+                if p["chunks_per_lane"] == 4:
+                    assert p["waves_per_token"] == 1 and p["block_threads"] == 256, (n, d, dt, p)
+                    assert p["tokens_per_block"] == 4
+                else:
+                    assert p["chunks_per_lane"] <= 2 and p["block_threads"] == 512, (n, d, dt, p)
+                    assert p["tokens_per_block"] * p["waves_per_token"] == 8
+    p = plan(_lib.OP_BWD, 9, 2048)
+    assert (p["waves_per_token"], p["chunks_per_lane"], p["rows_per_tile"]) == (1, 4, 9)
+    p = plan(_lib.OP_BWD, 16, 2048)  # no (1, 4, 16) tile: two waves, two chunks
+    assert (p["waves_per_token"], p["chunks_per_lane"], p["rows_per_tile"]) == (4, 1, 16)
 
 
 def test_batched_backward_plan():

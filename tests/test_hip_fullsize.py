@@ -167,7 +167,13 @@ def test_kernel_info_reports_the_persistent_grids():
     assert 0 < vgpr <= 256 and per_cu >= 1 and grid == min(cus * per_cu, b * t // 4)
     assert lib.sy_kernel_info(1, n, b * t, d, 2, 2, info) == 0
     vgpr, lds, per_cu, grid = list(info)
-    assert 0 < vgpr <= 256 and lds > 0 and grid == cus * per_cu
+    # The backward's (1, 4, 9) tile runs one wave per SIMD in 256-thread
+    # workgroups: up to 512 registers (VGPRs + AGPRs), one workgroup per CU.
+    bplan = _lib.plan(_lib.OP_BWD, n, d, torch.bfloat16)
+    waves_per_block = bplan["block_threads"] // 64
+    waves_per_simd = min(8, 512 // (-(-vgpr // 8) * 8))
+    assert 0 < vgpr <= 512 and lds > 0 and grid == cus * per_cu
+    assert per_cu == max(1, waves_per_simd * 4 // waves_per_block)
 
 
 def test_speed_of_light_and_probes():
