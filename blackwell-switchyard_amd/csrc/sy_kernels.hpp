@@ -603,10 +603,6 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
   constexpr uint32_t kStep = 64u * W * 16u;
   constexpr int kLaneFloats = VPL * CE;  // dw values a lane accumulates
   constexpr int G = STATS ? 1 : 3;       // per-row scalars reduced over D
-  // One wave per token with four chunks per lane runs at one wave per SIMD
-  // (512 registers): enough for a second token buffer, which keeps loads in
-  // flight through the reductions that no other wave on the SIMD would hide.
-  constexpr bool kTwoBuffers = W == 1 && VPL >= 4 && STATS;
   // Slot fold buffer: the upper half of the live slots parks its dw here. The
   // +1 pad keeps the lane-strided writes free of bank conflicts.
   constexpr int kFH = TPB > 1 ? TPB / 2 : 1;
@@ -647,33 +643,29 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
 #pragma unroll
     for (int e = 0; e < CE; ++e) dwa[j][e] = 0.0f;
 
-  // Load token slot k's rows and grad_out row into a register buffer.
-  auto load_token = [&](i32x4_t (&xb)[NR][VPL], i32x4_t (&gb)[VPL], int k) {
-    const int64_t t_raw = first + (int64_t)k * slots;
-    const int64_t t0 = t_raw < n_tok ? t_raw : n_tok - 1;
+  i32x4_t x[NR][VPL];
+  i32x4_t gq[VPL];
+  {
+    const int64_t t0 = first < n_tok ? first : n_tok - 1;
 #pragma unroll
     for (int n = 0; n < NR; ++n) {
       if (n < rows) {
         const auto r = make_rsrc(row_at<LISTED, const S>(v, n) + t0 * d, row_bytes);
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) xb[n][j] = ld16_stream(r, lane_off + j * kStep);
+        for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
       }
     }
     const auto gr = make_rsrc(g + t0 * d, row_bytes);
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) gb[j] = ld16_stream(gr, lane_off + j * kStep);
-  };
+    for (int j = 0; j < VPL; ++j) gq[j] = ld16_stream(gr, lane_off + j * kStep);
+  }
 
-  // One token: the row reductions, the softmax gradient, dv and the dw
-  // contribution. The buffer's registers are refilled with the slot's token
-  // `step` iterations ahead as soon as they have been consumed.
-  auto token = [&](i32x4_t (&x)[NR][VPL], i32x4_t (&gq)[VPL], int k, int step) {
+  for (int k = 0; k < iters; ++k) {
     const int64_t tok_raw = first + (int64_t)k * slots;
     const bool live = tok_raw < n_tok;
     const int64_t tok = live ? tok_raw : n_tok - 1;
-    const bool more = k + step < iters;
-    const int64_t ahead = tok_raw + (int64_t)step * slots;
-    const int64_t nxt = ahead < n_tok ? ahead : n_tok - 1;
+    const bool more = k + 1 < iters;
+    const int64_t nxt = tok_raw + slots < n_tok ? tok_raw + slots : n_tok - 1;
 
     // part[n] grad dot; without stats also part[NR + n] query dot and
     // part[2*NR + n] sum of squares.
@@ -794,23 +786,6 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
         }
       }
     }
-  };
-
-  i32x4_t x[NR][VPL];
-  i32x4_t gq[VPL];
-  load_token(x, gq, 0);
-  if constexpr (kTwoBuffers) {
-    // Two token buffers alternate: while one token is reduced, the next
-    // token's rows are already in flight in the other buffer.
-    i32x4_t x2[NR][VPL];
-    i32x4_t gq2[VPL];
-    if (iters > 1) load_token(x2, gq2, 1);
-    for (int k = 0; k < iters; k += 2) {
-      token(x, gq, k, 2);
-      if (k + 1 < iters) token(x2, gq2, k + 1, 2);
-    }
-  } else {
-    for (int k = 0; k < iters; ++k) token(x, gq, k, 1);
   }
 
   // Fold the TPB slot accumulators: slots [h, 2h) add into [0, h), h halving.

@@ -12,9 +12,9 @@
 //  3. Forward / speed-of-light with no resident fit: online-softmax chunks of
 //     the largest tile that fits.
 //  4. Backward: one wave per token with four chunks per lane when that covers
-//     the row (it runs at one wave per SIMD with 512 registers and two token
-//     buffers; fastest on MI355X: 62.5 vs 64.9 us at config 2); otherwise the
-//     two-waves-per-SIMD tiles under their budget; then generic.
+//     the row (it runs at one wave per SIMD with up to 512 registers; fastest
+//     on MI355X: 62.2 vs 64.9 us at config 2); otherwise the two-waves-per-SIMD
+//     tiles under their budget; then generic.
 //  5. Batched: resident with S <= 16, else one forward launch per query.
 //  6. Batched backward: one chunk per lane on the fewest waves that cover the
 //     row, N <= 9 and S <= 8 (dv and dq accumulators stay in registers);
