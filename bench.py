@@ -231,13 +231,17 @@ def cpu_baseline_leg(wl, args, torch):
     ts = min(512, wl.t)
     vs, gs = v[:, :, :ts].contiguous(), g[:, :ts].contiguous()
 
+    oracle_s = []  # float64 oracle forward + gradients on the slice, per call
+
     def ratios(wq):
         vt = vs.to(wl.dev).requires_grad_(True)
         wt = wq.to(wl.dev).requires_grad_(True)
         out = block_attn_res_hip(vt, wt)
         out.backward(gs.to(wl.dev))
+        t0 = time.perf_counter()
         o64 = oref.block_attn_res_oracle(vs, wq)
         dv64, dw64 = oref.oracle_grads(vs, wq, gs)
+        oracle_s.append(time.perf_counter() - t0)
         res = {}
         for name, got, ref in (("out", out, o64), ("dv", vt.grad, dv64), ("dw", wt.grad, dw64)):
             err, floor = oref.rel_l2(got, ref), oref.dtype_floor(ref, wl.dtype)
@@ -289,6 +293,8 @@ def cpu_baseline_leg(wl, args, torch):
                    f"after 1 warmup; {med * 1e3:.1f} ms per fwd+bwd"),
         "ms_per_step": med * 1e3,
         "host_cpu": None,
+        "host_logical_cpus": os.cpu_count(),
+        "oracle_f64_ms_per_512_tokens": round(min(oracle_s) * 1e3, 1),
     }
     return check, cpu
 

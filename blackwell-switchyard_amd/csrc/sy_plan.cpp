@@ -11,10 +11,10 @@
 //     with rows_per_tile >= N.
 //  3. Forward / speed-of-light with no resident fit: online-softmax chunks of
 //     the largest tile that fits.
-//  4. Backward: one wave per token with four chunks per lane when that covers
-//     the row (it runs at one wave per SIMD with up to 512 registers; fastest
-//     on MI355X: 62.2 vs 64.9 us at config 2); otherwise the two-waves-per-SIMD
-//     tiles under their budget; then generic.
+//  4. Backward with 5 <= N <= 9: one wave per token with four chunks per lane
+//     when that covers the row (it runs at one wave per SIMD with up to 512
+//     registers; fastest on MI355X: 62.2 vs 64.9 us at config 2); otherwise
+//     the two-waves-per-SIMD tiles under their budget; then generic.
 //  5. Batched: resident with S <= 16, else one forward launch per query.
 //  6. Batched backward: one chunk per lane on the fewest waves that cover the
 //     row, N <= 9 and S <= 8 (dv and dq accumulators stay in registers);
@@ -31,11 +31,14 @@ namespace {
 
 // Resident tile budget in 16-byte chunks per lane (4 VGPRs each). The
 // backward also keeps grad_out, w, their fp32 copies and dw accumulators live,
-// and the batched kernel a query and an accumulator, so both take a thinner
-// tile (more waves per token) than the forward.
+// so it takes a thinner tile (more waves per token) than the forward unless
+// one wave per token fits at one wave per SIMD (rule 4). The batched forward
+// holds a query and one accumulator next to the tile, like the forward, and
+// gains most from one wave per token: no cross-wave exchange per query
+// (config 3, 8 queries: 81.8 us at (1,4,9) vs 115.5 us at (2,2,9) on MI355X).
 constexpr int kFwdBudget = 36;
 constexpr int kBwdBudget = 18;
-constexpr int kBatchedBudget = 18;
+constexpr int kBatchedBudget = 36;
 constexpr int kWaves[] = {1, 2, 4, 8};
 constexpr int kRows[] = {4, 9, 16};
 
@@ -115,12 +118,11 @@ int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_
     return SY_OK;
   }
 
-  if (vec && op == SY_OP_BWD && e > 64 * 2 && e <= 64 * 4) {
-    for (int nr : kRows) {
-      if (nr < n_src || !tile_exists(4, nr)) continue;
-      set(out, SY_FAMILY_RESIDENT, 1, 4, nr, ce, op, n_src);
-      return SY_OK;
-    }
+  // One wave per token pays off from 5 rows on (N=9: 62.2 vs 64.9 us); with
+  // N <= 4 two waves of two chunks are as fast or faster (N=2: 25.9 vs 27.1 us).
+  if (vec && op == SY_OP_BWD && e > 64 * 2 && e <= 64 * 4 && n_src > 4 && n_src <= 9) {
+    set(out, SY_FAMILY_RESIDENT, 1, 4, 9, ce, op, n_src);
+    return SY_OK;
   }
   if (vec && !(op == SY_OP_BATCHED && n_q > kBatchedMaxQ)) {
     const int budget =

@@ -233,6 +233,8 @@ def test_backward_takes_four_chunks_only_with_one_wave_per_token():
                     assert p["tokens_per_block"] * p["waves_per_token"] == 8
     p = plan(_lib.OP_BWD, 9, 2048)
     assert (p["waves_per_token"], p["chunks_per_lane"], p["rows_per_tile"]) == (1, 4, 9)
+    p = plan(_lib.OP_BWD, 4, 2048)  # few rows: two waves of two chunks
+    assert (p["waves_per_token"], p["chunks_per_lane"], p["rows_per_tile"]) == (2, 2, 4)
     p = plan(_lib.OP_BWD, 16, 2048)  # no (1, 4, 16) tile: two waves, two chunks
     assert (p["waves_per_token"], p["chunks_per_lane"], p["rows_per_tile"]) == (4, 1, 16)
 
