@@ -205,7 +205,7 @@ int bwd_main_impl(const RowTable& v, bool v_ok, const void* w, const void* g, co
   if (n_tok == 0) return SY_OK;
   const bool aligned = vec_rows(v_ok && dv_ok, d, v_dtype) && al16(w) && al16(g) && al16(workspace);
   sy_plan p;
-  int rc = make_plan(SY_OP_BWD, n_src, 0, d, v_dtype, w_dtype, aligned, &p);
+  int rc = make_plan(SY_OP_BWD, n_src, 0, d, v_dtype, w_dtype, aligned, &p, stats != nullptr);
   if (rc != SY_OK) return rc;
   apply_tile_override(SY_OP_BWD, n_src, d, &p);
   int grid = 0;
@@ -351,20 +351,19 @@ int64_t sy_bwd_workspace_bytes(int64_t n_src, int64_t n_tok, int64_t d, int v_dt
   int rc = check_sizes(n_src, n_tok, d, v_dtype, w_dtype);
   if (rc != SY_OK) return rc;
   if (n_tok == 0) return 0;
-  // The vector plan assumes aligned buffers; a misaligned call falls back to
-  // the generic kernel with its own grid, so size for the larger of the two.
-  sy_plan pv, pg;
-  rc = make_plan(SY_OP_BWD, n_src, 0, d, v_dtype, w_dtype, 1, &pv);
-  if (rc != SY_OK) return rc;
-  apply_tile_override(SY_OP_BWD, n_src, d, &pv);
-  rc = make_plan(SY_OP_BWD, n_src, 0, d, v_dtype, w_dtype, 0, &pg);
-  if (rc != SY_OK) return rc;
+  // The vector plan assumes aligned buffers (a misaligned call falls back to
+  // the generic kernel with its own grid) and may depend on whether stats are
+  // passed, so size for the largest grid of every plan and variant.
   int64_t g = 0;
-  for (const sy_plan* pp : {&pv, &pg}) {
+  for (int aligned : {1, 0}) {
     for (bool st : {true, false}) {
+      sy_plan p;
+      rc = make_plan(SY_OP_BWD, n_src, 0, d, v_dtype, w_dtype, aligned, &p, st);
+      if (rc != SY_OK) return rc;
+      if (aligned) apply_tile_override(SY_OP_BWD, n_src, d, &p);
       for (int var : {0, 1, 2}) {
         int gi = 0;
-        rc = bwd_grid(*pp, n_tok, v_dtype, st, var, &gi);
+        rc = bwd_grid(p, n_tok, v_dtype, st, var, &gi);
         if (rc != SY_OK) return rc;
         if (gi > g) g = gi;
       }
@@ -448,7 +447,7 @@ int64_t sy_bwd_partial_rows(int64_t n_src, int64_t n_tok, int64_t d, int v_dtype
   if (rc != SY_OK) return rc;
   if (n_tok == 0) return 0;
   sy_plan p;
-  rc = make_plan(SY_OP_BWD, n_src, 0, d, v_dtype, w_dtype, aligned, &p);
+  rc = make_plan(SY_OP_BWD, n_src, 0, d, v_dtype, w_dtype, aligned, &p, has_stats != 0);
   if (rc != SY_OK) return rc;
   apply_tile_override(SY_OP_BWD, n_src, d, &p);
   int grid = 0;

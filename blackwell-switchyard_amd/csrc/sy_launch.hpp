@@ -100,9 +100,11 @@ struct BwdBatchedArgs {
   float eps;
 };
 
-// Pure shape arithmetic (sy_plan.cpp).
+// Pure shape arithmetic (sy_plan.cpp). `has_stats` matters to SY_OP_BWD only:
+// whether the forward's logits and r are passed (the operator's path, and what
+// sy_plan_for reports) or recomputed.
 int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_dtype, int aligned,
-              sy_plan* out);
+              sy_plan* out, int has_stats = 1);
 
 // Launch-time tile override from the SY_TILE_* environment variables
 // (sy_plan.cpp); sy_plan_for never applies it.

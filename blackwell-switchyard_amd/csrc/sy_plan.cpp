@@ -9,12 +9,18 @@
 //     (backward: 1 or 2) and whose resident tile (rows_per_tile x
 //     chunks_per_lane 16-byte chunks, four VGPRs each) fits the op's budget
 //     with rows_per_tile >= N.
-//  3. Forward / speed-of-light with no resident fit: online-softmax chunks of
-//     the largest tile that fits.
-//  4. Backward with 5 <= N <= 9: one wave per token with four chunks per lane
-//     when that covers the row (it runs at one wave per SIMD with up to 512
-//     registers; fastest on MI355X: 62.2 vs 64.9 us at config 2); otherwise
-//     the two-waves-per-SIMD tiles under their budget; then generic.
+//  3. Forward / speed-of-light whose fewest-waves tile has four chunks per
+//     lane but no resident fit (N > 9): online-softmax chunks of 4 rows at
+//     that wave count, rather than more waves per token (N=16: 49.9 vs 74.9 us
+//     for the resident (2,2,16) tile on MI355X). No resident fit at any wave
+//     count: online-softmax chunks of the largest tile that fits.
+//  4. Backward with 5 <= N <= 9: four chunks per lane on the 1, 2 or 4 waves
+//     that cover the row, one wave per SIMD with up to 512 registers (config 2:
+//     62.2 vs 64.9 us; D=4096: 130.1 vs 134.0 us); otherwise the
+//     two-waves-per-SIMD tiles under their budget; then generic. The budget
+//     admits 16 rows x 2 chunks when the forward's stats are passed (that
+//     variant holds no recompute state and fits 256 VGPRs; N=16: 128.7 vs
+//     168.2 us); without stats that tile spills and the thinner one is kept.
 //  5. Batched: resident with S <= 16, else one forward launch per query.
 //  6. Batched backward: one chunk per lane on the fewest waves that cover the
 //     row, N <= 9 and S <= 8 (dv and dq accumulators stay in registers);
@@ -38,6 +44,7 @@ namespace {
 // (config 3, 8 queries: 81.8 us at (1,4,9) vs 115.5 us at (2,2,9) on MI355X).
 constexpr int kFwdBudget = 36;
 constexpr int kBwdBudget = 18;
+constexpr int kBwdStatsBudget = 32;
 constexpr int kBatchedBudget = 36;
 constexpr int kWaves[] = {1, 2, 4, 8};
 constexpr int kRows[] = {4, 9, 16};
@@ -91,7 +98,7 @@ bool resident(int64_t n_src, int64_t e, int budget, int max_vpl, int* w_out, int
 }  // namespace
 
 int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_dtype,
-              int aligned, sy_plan* out) {
+              int aligned, sy_plan* out, int has_stats) {
   if (out == nullptr) return SY_ERR_NULL;
   if (op < SY_OP_FWD || op > SY_OP_BWD_BATCHED) return SY_ERR_OP;
   if (!valid_dtype(v_dtype) || !valid_dtype(w_dtype)) return SY_ERR_DTYPE;
@@ -118,18 +125,36 @@ int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_
     return SY_OK;
   }
 
-  // One wave per token pays off from 5 rows on (N=9: 62.2 vs 64.9 us); with
-  // N <= 4 two waves of two chunks are as fast or faster (N=2: 25.9 vs 27.1 us).
-  if (vec && op == SY_OP_BWD && e > 64 * 2 && e <= 64 * 4 && n_src > 4 && n_src <= 9) {
-    set(out, SY_FAMILY_RESIDENT, 1, 4, 9, ce, op, n_src);
-    return SY_OK;
+  // Four chunks per lane at one wave per SIMD pay off from 5 rows on (N=9:
+  // 62.2 vs 64.9 us); with N <= 4 two chunks on twice the waves are as fast or
+  // faster (N=2: 25.9 vs 27.1 us). Eight waves of such a tile would share a
+  // SIMD and spill.
+  if (vec && op == SY_OP_BWD && n_src > 4 && n_src <= 9) {
+    for (int ww : {1, 2, 4}) {
+      if (e > 64 * 2 * ww && e <= 64 * 4 * ww) {
+        set(out, SY_FAMILY_RESIDENT, ww, 4, 9, ce, op, n_src);
+        return SY_OK;
+      }
+    }
   }
   if (vec && !(op == SY_OP_BATCHED && n_q > kBatchedMaxQ)) {
-    const int budget =
-        op == SY_OP_BWD ? kBwdBudget : (op == SY_OP_BATCHED ? kBatchedBudget : kFwdBudget);
+    const int budget = op == SY_OP_BWD     ? (has_stats ? kBwdStatsBudget : kBwdBudget)
+                       : op == SY_OP_BATCHED ? kBatchedBudget
+                                             : kFwdBudget;
     // The backward keeps grad_out, w (raw and fp32) and dw accumulators next
     // to the tile: with 4 chunks per lane some of its variants spill.
     const int max_vpl = op == SY_OP_BWD ? 2 : 4;
+    if ((op == SY_OP_FWD || op == SY_OP_SOL) && n_src > 9) {
+      for (int ww : kWaves) {
+        const int v2 = round_vpl((e + 64 * ww - 1) / (64 * ww));
+        if (v2 == 0) continue;
+        if (v2 == 4) {
+          set(out, SY_FAMILY_CHUNKED, ww, 4, 4, ce, op, n_src);
+          return SY_OK;
+        }
+        break;
+      }
+    }
     if (resident(n_src, e, budget, max_vpl, &w, &vpl, &nr)) {
       set(out, SY_FAMILY_RESIDENT, w, vpl, nr, ce, op, n_src);
       return SY_OK;
@@ -138,7 +163,7 @@ int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_
       for (int ww : kWaves) {
         const int v2 = round_vpl((e + 64 * ww - 1) / (64 * ww));
         if (v2 == 0) continue;
-        set(out, SY_FAMILY_CHUNKED, ww, v2, v2 == 4 ? 9 : 16, ce, op, n_src);
+        set(out, SY_FAMILY_CHUNKED, ww, v2, v2 == 4 ? 4 : 16, ce, op, n_src);
         return SY_OK;
       }
     }

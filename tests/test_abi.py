@@ -178,7 +178,17 @@ def test_representative_shape_is_register_resident_everywhere():
 
 @pytest.mark.parametrize("n,d", [(9, 4096), (16, 2048), (9, 8192), (16, 4096), (4, 1024), (1, 256)])
 def test_sweep_shapes_stay_resident_in_both_directions(n, d):
-    assert plan(_lib.OP_FWD, n, d)["family_name"] == "resident"
+    """Every sweep shape's backward holds all rows in registers; so does the
+    forward up to 9 rows. Past 9 rows the forward keeps one wave's four chunks
+    per lane and runs online-softmax chunks of 4 rows instead of spreading the
+    token over more waves."""
+    f = plan(_lib.OP_FWD, n, d)
+    if n <= 9:
+        assert f["family_name"] == "resident"
+    else:
+        assert f["family_name"] == "chunked" and f["chunks_per_lane"] == 4
+        assert f["rows_per_tile"] == 4 and f["n_chunks"] == (n + 3) // 4
+        assert f["waves_per_token"] == d // 2048
     assert plan(_lib.OP_BWD, n, d)["family_name"] == "resident"
 
 
@@ -216,27 +226,34 @@ def test_batched_query_cap():
     assert plan(_lib.OP_BATCHED, 9, 2048, n_q=17)["family_name"] == "per_query"
 
 
-def test_backward_takes_four_chunks_only_with_one_wave_per_token():
+def test_backward_takes_four_chunks_only_with_one_wave_per_simd():
     """Four chunks per lane run one wave per SIMD (256-thread workgroups, 512
-    registers); every other backward tile runs two waves per SIMD (512 threads)."""
-    for n in (1, 2, 4, 9, 16):
+    registers, at most 4 waves per token); every other backward tile runs two
+    waves per SIMD (512 threads)."""
+    for n in (1, 2, 4, 5, 9, 12, 16):
         for d in (512, 1024, 1536, 2048, 4096, 8192):
             for dt in (torch.bfloat16, torch.float32):
                 p = plan(_lib.OP_BWD, n, d, dt)
                 if p["family_name"] != "resident":
                     continue
                 if p["chunks_per_lane"] == 4:
-                    assert p["waves_per_token"] == 1 and p["block_threads"] == 256, (n, d, dt, p)
-                    assert p["tokens_per_block"] == 4
+                    assert 5 <= n <= 9 and p["rows_per_tile"] == 9, (n, d, dt, p)
+                    assert p["waves_per_token"] <= 4 and p["block_threads"] == 256, (n, d, dt, p)
+                    assert p["tokens_per_block"] * p["waves_per_token"] == 4
                 else:
                     assert p["chunks_per_lane"] <= 2 and p["block_threads"] == 512, (n, d, dt, p)
                     assert p["tokens_per_block"] * p["waves_per_token"] == 8
-    p = plan(_lib.OP_BWD, 9, 2048)
-    assert (p["waves_per_token"], p["chunks_per_lane"], p["rows_per_tile"]) == (1, 4, 9)
-    p = plan(_lib.OP_BWD, 4, 2048)  # few rows: two waves of two chunks
-    assert (p["waves_per_token"], p["chunks_per_lane"], p["rows_per_tile"]) == (2, 2, 4)
-    p = plan(_lib.OP_BWD, 16, 2048)  # no (1, 4, 16) tile: two waves, two chunks
-    assert (p["waves_per_token"], p["chunks_per_lane"], p["rows_per_tile"]) == (4, 1, 16)
+    tile = lambda p: (p["waves_per_token"], p["chunks_per_lane"], p["rows_per_tile"])
+    assert tile(plan(_lib.OP_BWD, 9, 2048)) == (1, 4, 9)
+    assert tile(plan(_lib.OP_BWD, 9, 4096)) == (2, 4, 9)
+    assert tile(plan(_lib.OP_BWD, 9, 2048, torch.float32)) == (2, 4, 9)
+    assert tile(plan(_lib.OP_BWD, 9, 8192)) == (4, 4, 9)
+    assert tile(plan(_lib.OP_BWD, 9, 16384))[1] <= 2  # eight such waves would share a SIMD
+    assert tile(plan(_lib.OP_BWD, 4, 2048)) == (2, 2, 4)  # few rows: two waves of two chunks
+    # 16 rows x 2 chunks: the with-stats variant (what the plan reports) fits.
+    assert tile(plan(_lib.OP_BWD, 16, 2048)) == (2, 2, 16)
+    assert tile(plan(_lib.OP_BWD, 12, 2048)) == (2, 2, 16)
+    assert tile(plan(_lib.OP_BWD, 16, 4096)) == (4, 2, 16)
 
 
 def test_batched_backward_plan():

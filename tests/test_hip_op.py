@@ -61,6 +61,7 @@ SHAPES = [
     (9, 1, 512, 1024), (9, 1, 256, 2048), (9, 1, 128, 4096), (9, 1, 64, 8192),
     (16, 1, 128, 1024), (17, 1, 64, 2048), (32, 1, 64, 1024), (33, 1, 64, 512),
     (3, 1, 64, 777), (5, 1, 17, 63), (8, 3, 101, 1536), (7, 2, 1, 320),
+    (12, 1, 64, 2048), (16, 1, 64, 2048), (16, 1, 32, 4096),
 ]
 
 
@@ -283,3 +284,42 @@ def test_dispatch_sends_the_representative_shape_to_the_resident_kernels():
     assert _launch_config(9, 2048)[0], "N=9, D=2048 forward must be register-resident"
     assert _bwd_launch(9, 2048)[0], "N=9, D=2048 backward must be register-resident"
     assert _bwd_launch(9, 4096)[0], "N=9, D=4096 backward is resident on MI355X too"
+
+
+@pytest.mark.parametrize("shape", [(16, 1, 64, 2048), (12, 1, 96, 2048), (16, 1, 32, 4096),
+                                   (9, 1, 64, 4096), (9, 1, 32, 8192), (9, 1, 64, 2048)])
+def test_backward_with_and_without_forward_stats_matches_the_oracle(shape):
+    """The backward may run a different tile when the forward's stats are not
+    passed (16 rows: a thinner tile that holds the recompute state); both
+    paths through the C ABI sit at the bf16 floor."""
+    import ctypes
+
+    from switchyard import _lib
+
+    n, b, t, d = shape
+    nt = b * t
+    gen = torch.Generator().manual_seed(11)
+    v = torch.randn(n, b, t, d, generator=gen).to(torch.bfloat16)
+    w = (0.5 * torch.randn(d, generator=gen)).to(torch.bfloat16)
+    g = torch.randn(b, t, d, generator=gen).to(torch.bfloat16)
+    dv64, dw64 = oracle_grads(v, w, g)
+    lib = _lib.lib()
+    vd, wd, gd = v.to(DEV), w.to(DEV), g.to(DEV)
+    ptr = lambda x: None if x is None else ctypes.c_void_p(x.data_ptr())
+    stream = _lib.stream_ptr(DEV)
+    out = torch.empty(b, t, d, device=DEV, dtype=torch.bfloat16)
+    stats = torch.empty(2, n, nt, device=DEV)
+    assert lib.sy_fwd(ptr(vd), ptr(wd), ptr(out), ptr(stats), n, nt, d, nt * d, 2, 2, 1e-6, stream) == 0
+    ws_bytes = lib.sy_bwd_workspace_bytes(n, nt, d, 2, 2)
+    ws = torch.empty(ws_bytes // 4, device=DEV)
+    for st in (stats, None):
+        dv = torch.empty_like(vd)
+        dw = torch.empty(d, device=DEV, dtype=torch.bfloat16)
+        rows = lib.sy_bwd_partial_rows(n, nt, d, 2, 2, 1, int(st is not None))
+        assert 0 < rows and rows * d * 4 <= ws_bytes
+        assert lib.sy_bwd(ptr(vd), ptr(wd), ptr(gd), ptr(st), ptr(dv), ptr(dw), ptr(ws), ws_bytes,
+                          n, nt, d, nt * d, 2, 2, 1e-6, stream) == 0
+        torch.cuda.synchronize()
+        for name, got, want in (("dv", dv, dv64), ("dw", dw, dw64)):
+            err, floor = rel_l2(got, want), dtype_floor(want, torch.bfloat16)
+            assert err <= _bound(floor, torch.bfloat16), (name, st is None, err, floor)
