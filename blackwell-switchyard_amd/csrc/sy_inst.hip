@@ -142,6 +142,7 @@ hipError_t SY_FN(bwd_vec_resources_)(const sy_plan& p, bool stats, int variant, 
     return hipSuccess;                                                                       \
   }
   SY_TILES(X)
+  SY_BWD_WIDE_TILES(X)
 #undef X
   return hipErrorInvalidConfiguration;
 }
@@ -169,6 +170,7 @@ hipError_t SY_FN(launch_bwd_vec_)(const sy_plan& p, const BwdArgs& a, int grid, 
     return hipGetLastError();                                                                \
   }
   SY_TILES(X)
+  SY_BWD_WIDE_TILES(X)
 #undef X
 #undef SY_BWD_LAUNCH
   return hipErrorInvalidConfiguration;

@@ -582,7 +582,11 @@ k_sol_res(const RowTable v, typename T::storage* __restrict__ out, int n_src, in
 // per-row pointers cost two SGPRs a row and the (o, m, l) algebra extra VALU,
 // which the operator's kernel does not pay.
 // grad_out and each source row are refilled with the next token's data as soon
-// as they have been consumed.
+// as they have been consumed. The per-token scalars (logit_n and r_n from the
+// stats, and gm/gl) are fetched one token ahead by a single vector load, lane
+// i < 16 holding logit_i, lane 16 + i r_i, lanes 32/33 gm/gl, and broadcast
+// with readlane: read as uniform scalars they would be scalar loads waited on
+// one by one in every token's critical path.
 // dw: each slot accumulates in registers; at the end the slots are folded in
 // a fixed tree through LDS and the workgroup writes one fp32 row of `partial`.
 // No float atomics anywhere, so dw is bit-reproducible for a given grid.
@@ -659,6 +663,21 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
 #pragma unroll
     for (int j = 0; j < VPL; ++j) gq[j] = ld16_stream(gr, lane_off + j * kStep);
   }
+  static_assert(NR <= 16, "token scalars are spread over lanes 0..33");
+  // The token scalars of token t for this lane (see above); 0 for idle lanes.
+  auto scalars_of = [&](int64_t t) -> float {
+    const int i = lane & 15;
+    if constexpr (STATS) {
+      if (lane < 32 && i < rows) return stats[(int64_t)((lane >> 4) * n_src + i) * n_tok + t];
+    }
+    if constexpr (GRAD_STATS) {
+      if (lane == 32) return gm[t];
+      if (lane == 33) return gl[t];
+    }
+    return 0.0f;
+  };
+  [[maybe_unused]] float sc_next = 0.0f;
+  if constexpr (STATS || GRAD_STATS) sc_next = scalars_of(first < n_tok ? first : n_tok - 1);
 
   for (int k = 0; k < iters; ++k) {
     const int64_t tok_raw = first + (int64_t)k * slots;
@@ -666,6 +685,13 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
     const int64_t tok = live ? tok_raw : n_tok - 1;
     const bool more = k + 1 < iters;
     const int64_t nxt = tok_raw + slots < n_tok ? tok_raw + slots : n_tok - 1;
+    [[maybe_unused]] const float sc = sc_next;
+    if constexpr (STATS || GRAD_STATS) {
+      if (more) sc_next = scalars_of(nxt);
+    }
+    auto scalar = [&](int i) -> float {
+      return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sc), i));
+    };
 
     // part[n] grad dot; without stats also part[NR + n] query dot and
     // part[2*NR + n] sum of squares.
@@ -703,8 +729,8 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
     for (int n = 0; n < NR; ++n) {
       if (n < rows) {
         if constexpr (STATS) {
-          lg[n] = stats[(int64_t)n * n_tok + tok];
-          rr[n] = stats[(int64_t)(n_src + n) * n_tok + tok];
+          lg[n] = scalar(n);
+          rr[n] = scalar(16 + n);
         } else {
           rr[n] = rsqrtf(fmaf(part[2 * NR + n], inv_d, eps));
           lg[n] = part[NR + n] * rr[n];
@@ -736,7 +762,7 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
           sdev = fmaf(al[n], part[n], sdev);
         }
     } else {
-      const float glv = gl[tok], gmv = gm[tok];
+      const float glv = scalar(33), gmv = scalar(32);
       float other = 0.0f;
 #pragma unroll
       for (int n = 0; n < NR; ++n)

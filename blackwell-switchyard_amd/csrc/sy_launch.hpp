@@ -19,6 +19,10 @@ namespace sy {
   X(4, 1, 4) X(4, 1, 9) X(4, 1, 16) X(4, 2, 4) X(4, 2, 9) X(4, 2, 16) X(4, 4, 4) X(4, 4, 9) \
   X(8, 1, 4) X(8, 1, 9) X(8, 1, 16) X(8, 2, 4) X(8, 2, 9) X(8, 2, 16) X(8, 4, 4) X(8, 4, 9)
 
+// Backward-only tiles with four chunks per lane and 16 rows: 256 tile VGPRs,
+// which fit only at one wave per SIMD (512 registers, 256-thread workgroups).
+#define SY_BWD_WIDE_TILES(X) X(1, 4, 16) X(2, 4, 16)
+
 // Largest N the generic kernels accept (their per-token scalars live in LDS).
 constexpr int64_t kGenericMaxN = 4096;
 // Largest query count of the resident batched kernel.

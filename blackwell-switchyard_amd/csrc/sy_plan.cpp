@@ -14,13 +14,14 @@
 //     that wave count, rather than more waves per token (N=16: 49.9 vs 74.9 us
 //     for the resident (2,2,16) tile on MI355X). No resident fit at any wave
 //     count: online-softmax chunks of the largest tile that fits.
-//  4. Backward with 5 <= N <= 9: four chunks per lane on the 1, 2 or 4 waves
-//     that cover the row, one wave per SIMD with up to 512 registers (config 2:
-//     62.2 vs 64.9 us; D=4096: 130.1 vs 134.0 us); otherwise the
-//     two-waves-per-SIMD tiles under their budget; then generic. The budget
+//  4. Backward with 5 <= N <= 16: four chunks per lane on the waves that cover
+//     the row (1, 2 or 4 waves for 9 rows, 1 or 2 for 16), one wave per SIMD
+//     with up to 512 registers (config 2: 62.2 vs 64.9 us; D=4096: 130.1 vs
+//     134.0 us; N=16: 106.3 vs 113.8 us for (2,2,16)). Otherwise the
+//     two-waves-per-SIMD tiles under their budget, then generic. The budget
 //     admits 16 rows x 2 chunks when the forward's stats are passed (that
-//     variant holds no recompute state and fits 256 VGPRs; N=16: 128.7 vs
-//     168.2 us); without stats that tile spills and the thinner one is kept.
+//     variant holds no recompute state and fits 256 VGPRs); without stats that
+//     tile spills and the thinner one is kept.
 //  5. Batched: resident with S <= 16, else one forward launch per query.
 //  6. Batched backward: one chunk per lane on the fewest waves that cover the
 //     row, N <= 9 and S <= 8 (dv and dq accumulators stay in registers);
@@ -126,13 +127,16 @@ int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_
   }
 
   // Four chunks per lane at one wave per SIMD pay off from 5 rows on (N=9:
-  // 62.2 vs 64.9 us); with N <= 4 two chunks on twice the waves are as fast or
-  // faster (N=2: 25.9 vs 27.1 us). Eight waves of such a tile would share a
-  // SIMD and spill.
-  if (vec && op == SY_OP_BWD && n_src > 4 && n_src <= 9) {
+  // 62.2 vs 64.9 us); with N <= 4 two chunks on twice the waves are faster
+  // (N=4: 36.4 vs 38.4 us, N=2: 24.6 vs 27.7 us). Eight waves of such a tile
+  // would share a SIMD and spill. The 16-row tile holds 256 VGPRs of source
+  // rows: its recompute variant (no stats) spills 68 bytes a lane and still
+  // beats the thinner tiles (N=16: 119 vs 167 us).
+  if (vec && op == SY_OP_BWD && n_src > 4 && n_src <= 16) {
     for (int ww : {1, 2, 4}) {
+      if (n_src > 9 && ww == 4) break;
       if (e > 64 * 2 * ww && e <= 64 * 4 * ww) {
-        set(out, SY_FAMILY_RESIDENT, ww, 4, 9, ce, op, n_src);
+        set(out, SY_FAMILY_RESIDENT, ww, 4, n_src <= 9 ? 9 : 16, ce, op, n_src);
         return SY_OK;
       }
     }
@@ -180,10 +184,13 @@ int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_
   return SY_OK;
 }
 
-bool tile_listed(int w, int vpl, int nr) {
+bool tile_listed(int op, int w, int vpl, int nr) {
 #define X(W_, V_, N_) \
   if (w == W_ && vpl == V_ && nr == N_) return true;
   SY_TILES(X)
+  if (op == SY_OP_BWD) {
+    SY_BWD_WIDE_TILES(X)
+  }
 #undef X
   return false;
 }
@@ -201,7 +208,7 @@ void apply_tile_override(int op, int64_t n_src, int64_t d, sy_plan* p) {
   const char* s = std::getenv(name);
   int w = 0, vpl = 0, nr = 0;
   if (s == nullptr || std::sscanf(s, "%d,%d,%d", &w, &vpl, &nr) != 3) return;
-  if (!tile_listed(w, vpl, nr)) return;
+  if (!tile_listed(op, w, vpl, nr)) return;
   if ((int64_t)64 * w * vpl < d / p->elems_per_chunk) return;
   const bool can_chunk = op == SY_OP_FWD || op == SY_OP_SOL;
   if (nr < n_src && !can_chunk) return;

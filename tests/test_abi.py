@@ -237,8 +237,9 @@ def test_backward_takes_four_chunks_only_with_one_wave_per_simd():
                 if p["family_name"] != "resident":
                     continue
                 if p["chunks_per_lane"] == 4:
-                    assert 5 <= n <= 9 and p["rows_per_tile"] == 9, (n, d, dt, p)
-                    assert p["waves_per_token"] <= 4 and p["block_threads"] == 256, (n, d, dt, p)
+                    assert 5 <= n <= 16 and p["rows_per_tile"] == (9 if n <= 9 else 16), (n, d, dt, p)
+                    assert p["waves_per_token"] <= (4 if n <= 9 else 2), (n, d, dt, p)
+                    assert p["block_threads"] == 256, (n, d, dt, p)
                     assert p["tokens_per_block"] * p["waves_per_token"] == 4
                 else:
                     assert p["chunks_per_lane"] <= 2 and p["block_threads"] == 512, (n, d, dt, p)
@@ -250,10 +251,13 @@ def test_backward_takes_four_chunks_only_with_one_wave_per_simd():
     assert tile(plan(_lib.OP_BWD, 9, 8192)) == (4, 4, 9)
     assert tile(plan(_lib.OP_BWD, 9, 16384))[1] <= 2  # eight such waves would share a SIMD
     assert tile(plan(_lib.OP_BWD, 4, 2048)) == (2, 2, 4)  # few rows: two waves of two chunks
-    # 16 rows x 2 chunks: the with-stats variant (what the plan reports) fits.
-    assert tile(plan(_lib.OP_BWD, 16, 2048)) == (2, 2, 16)
-    assert tile(plan(_lib.OP_BWD, 12, 2048)) == (2, 2, 16)
-    assert tile(plan(_lib.OP_BWD, 16, 4096)) == (4, 2, 16)
+    assert tile(plan(_lib.OP_BWD, 16, 2048)) == (1, 4, 16)
+    assert tile(plan(_lib.OP_BWD, 12, 2048)) == (1, 4, 16)
+    assert tile(plan(_lib.OP_BWD, 16, 4096)) == (2, 4, 16)
+    # No four-chunk 16-row tile on four waves: 16 rows x 2 chunks on eight,
+    # which the with-stats variant (what the plan reports) fits.
+    assert tile(plan(_lib.OP_BWD, 16, 8192)) == (8, 2, 16)
+    assert tile(plan(_lib.OP_BWD, 16, 1024)) == (1, 2, 16)
 
 
 def test_batched_backward_plan():

@@ -63,7 +63,8 @@ def _np(x):
     return x.detach().double().cpu().numpy()
 
 
-SHAPES = [(1, 32, 256), (4, 64, 512), (9, 128, 2048), (16, 40, 1024), (5, 33, 777), (20, 16, 512)]
+SHAPES = [(1, 32, 256), (4, 64, 512), (9, 128, 2048), (16, 40, 1024), (5, 33, 777), (20, 16, 512),
+          (16, 48, 2048), (12, 24, 4096)]
 
 
 # -- attn_with_stats ---------------------------------------------------------

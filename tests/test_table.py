@@ -42,7 +42,7 @@ def _separate(v):
 
 
 SHAPES = [(1, 1, 64, 256), (5, 2, 33, 512), (9, 1, 256, 2048), (16, 1, 64, 1024),
-          (3, 1, 40, 777), (9, 1, 64, 4096)]
+          (3, 1, 40, 777), (9, 1, 64, 4096), (16, 1, 64, 2048), (12, 1, 32, 4096)]
 
 
 @pytest.mark.parametrize("shape", SHAPES)
