@@ -247,10 +247,14 @@ int batched_impl(const RowTable& v, bool v_ok, const void* q, void* out, float* 
   if (rc != SY_OK) return rc;
   apply_tile_override(SY_OP_BATCHED, n_src, d, &p);
   if (n_tok == 0) return SY_OK;
-  if (p.family == SY_FAMILY_RESIDENT) {
+  // The matrix kernel's store offsets are 32-bit; past that, per-query launches.
+  if (p.family == SY_FAMILY_MATRIX && !matrix_batched_offsets_fit(n_q, n_tok, d))
+    p.family = SY_FAMILY_PER_QUERY;
+  if (p.family == SY_FAMILY_RESIDENT || p.family == SY_FAMILY_MATRIX) {
     const BatchedArgs a{v,          q,        out,   m_out,  l_out, normalize,
                         (int)n_src, (int)n_q, n_tok, (int)d, dtype, eps};
-    return status(batched_vec(p, a, s));
+    return status(p.family == SY_FAMILY_MATRIX ? launch_batched_matrix(a, s, nullptr)
+                                               : batched_vec(p, a, s));
   }
   const int64_t es = esize(dtype);
   for (int64_t k = 0; k < n_q; ++k) {

@@ -30,6 +30,24 @@ constexpr int64_t kBatchedMaxQ = 16;
 // Register-resident batched backward: at most this many sources and queries.
 constexpr int64_t kBwdBatchedMaxN = 9;
 constexpr int64_t kBwdBatchedMaxQ = 8;
+// Batched forward on the matrix cores (sy_matrix.hip): 16-bit inputs, at most
+// 16 sources and 16 queries (one MFMA tile each way), D in {512, 1024, 1536,
+// 2048} (four waves x 32-column MFMA steps; a wave keeps its query slice in
+// registers). Its stores address four query rows from one buffer resource, so
+// 4 * n_tok * D * 2 bytes must stay below 2^31 (else the per-query path runs).
+// Below kMatrixMinQ queries the register-tiled kernel is faster (config 3
+// shape, MI355X: 2 queries 38.0 vs 67.9 us; 8 queries 82.5 vs 75.5 us).
+constexpr int64_t kMatrixMaxRows = 16;
+constexpr int64_t kMatrixMaxQ = 16;
+constexpr int64_t kMatrixMinQ = 6;
+inline bool matrix_batched_fits(int64_t n_src, int64_t n_q, int64_t d, int dtype) {
+  return (dtype == SY_BF16 || dtype == SY_F16) && n_src >= 1 && n_src <= kMatrixMaxRows &&
+         n_q >= kMatrixMinQ && n_q <= kMatrixMaxQ &&
+         (d == 512 || d == 1024 || d == 1536 || d == 2048);
+}
+inline bool matrix_batched_offsets_fit(int64_t n_q, int64_t n_tok, int64_t d) {
+  return 4 * n_tok * d * 2 < ((int64_t)1 << 31) && n_q * n_tok * 4 < ((int64_t)1 << 31);
+}
 // Dynamic LDS the generic kernels may request (bytes).
 constexpr int64_t kGenericMaxLds = 64 * 1024;
 // LDS of the generic batched backward: per-(query, row) alpha and da, per-row
@@ -113,6 +131,11 @@ int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_
 // Launch-time tile override from the SY_TILE_* environment variables
 // (sy_plan.cpp); sy_plan_for never applies it.
 void apply_tile_override(int op, int64_t n_src, int64_t d, sy_plan* p);
+
+// Launches the matrix-core batched forward (a.n_src etc. must pass
+// matrix_batched_fits). With `info` != nullptr fills it and launches nothing.
+struct KernelRes;
+hipError_t launch_batched_matrix(const BatchedArgs& a, hipStream_t s, KernelRes* info);
 
 // Device queries, cached per device (sy_capi.cpp).
 hipError_t cu_count(int* out);

@@ -1,0 +1,371 @@
+// Batched forward on the matrix cores (bf16 / fp16 inputs).
+//
+// With S queries the batched operator does S dot products and S weighted sums
+// per source row: 8 queries x 9 rows at D=2048 cost ~7000 VALU instructions a
+// token in the register-tiled kernel, which makes it VALU-bound at half the
+// HBM rate. Both products are small matrix products per token, so here they run
+// on MFMA:
+//   logits   L^T[n][s] = sum_d V[n][d] Q[s][d]   v_mfma_f32_16x16x32 (K = d)
+//   output   O^T[d][s] = sum_n V[n][d] P[s][n]   v_mfma_f32_16x16x16 (K = n)
+// with N <= 16 sources on one MFMA dimension and S <= 16 queries on the other.
+// V and Q are exact in the 16-bit operands and every product accumulates in
+// fp32. P (the softmax numerators, fp32) is split into a 16-bit high part and
+// the 16-bit rounding of its remainder, two MFMAs per output block, so the
+// weights carry ~17 significant bits and the output keeps fp32-level error
+// before its single rounding.
+//
+// Work split: a workgroup of 4 waves owns one token at a time (persistent over
+// tokens); wave w owns the D/4 columns [w*D/4, (w+1)*D/4). Its slice of the
+// queries stays in registers for the whole kernel (B operand of the logits),
+// its slice of the token's rows goes to LDS, row-major, and is read twice: as
+// 16-byte row chunks for the logits and through ds_read_b64_tr_b16 (a 4x4
+// transpose of 16-bit elements within each 16-lane group) as the n-packed A
+// operand of the output product. Each wave reads back only what it wrote, so V
+// needs no barrier; the per-wave logit and sum-of-squares partials are summed
+// through LDS once per token (one barrier, double-buffered). The next token's
+// rows are loaded into registers while the current one is computed and
+// written to LDS when it is done.
+//
+// Reference: the batched forward of src/switchyard/triton_op.py:378-501 (same
+// math as S calls of the single-query operator, one read of v).
+#include <algorithm>
+
+#include "sy_launch.hpp"
+
+namespace sy {
+
+namespace {
+
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x2_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+
+constexpr int kMxWaves = 4;                               // waves per workgroup, one token
+constexpr int kMxRows = (int)kMatrixMaxRows;              // MFMA M of the logits, K of the output
+constexpr int kMxPad = 64;                                // LDS row padding (bytes)
+constexpr int kMxGroup = 4;  // 32-column output blocks staged in LDS per store round
+
+template <class T> struct Mx;
+template <> struct Mx<BF16> {
+  static __device__ __forceinline__ f32x4_t k32(const i32x4_t& a, const i32x4_t& b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4_t k16(const i32x2_t& a, const i32x2_t& b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, a),
+                                                     __builtin_bit_cast(bf16x4_t, b), c, 0, 0, 0);
+  }
+  // Round two values (x in the low half) and read the halves back as fp32.
+  static __device__ __forceinline__ int pack2(float x, float y) {
+    const f32x2_t p = {x, y};
+    return __builtin_bit_cast(int, __builtin_convertvector(p, bf16x2_t));
+  }
+  static __device__ __forceinline__ float lo(int w) { return __uint_as_float((uint32_t)w << 16); }
+  static __device__ __forceinline__ float hi(int w) {
+    return __uint_as_float((uint32_t)w & 0xffff0000u);
+  }
+};
+template <> struct Mx<F16> {
+  static __device__ __forceinline__ f32x4_t k32(const i32x4_t& a, const i32x4_t& b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4_t k16(const i32x2_t& a, const i32x2_t& b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, a),
+                                                 __builtin_bit_cast(f16x4_t, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ int pack2(float x, float y) {
+    const f32x2_t p = {x, y};
+    return __builtin_bit_cast(int, __builtin_convertvector(p, f16x2_t));
+  }
+  static __device__ __forceinline__ float lo(int w) {
+    return (float)__builtin_bit_cast(f16x2_t, w).x;
+  }
+  static __device__ __forceinline__ float hi(int w) {
+    return (float)__builtin_bit_cast(f16x2_t, w).y;
+  }
+};
+
+// Orders this wave's LDS accesses across lanes: rows written by one lane are
+// read by others in the same wave, with no workgroup barrier in between.
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// LDS: [n_src + 1][d * 2 + kMxPad] bytes of rows (the extra row is zero and
+// stands in for rows n >= n_src), then the exchange buffers. KS = D / 128
+// (32-column steps of a wave), NR >= n_src staged rows. Two tokens are in
+// flight per workgroup while a third is computed; the loop is unrolled by two
+// so that both staging sets keep compile-time register indices.
+//
+// Every global load and store in the loop is issued unconditionally (missing
+// rows load through a zero-size resource, masked lanes store past the end of
+// theirs), so the number of memory operations between a prefetch and its use
+// is a compile-time constant and the compiler waits for exactly the prefetch,
+// not for everything in flight.
+template <class T, int KS, int NR>
+__global__ void __launch_bounds__(256, 2)
+k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restrict__ out,
+             float* __restrict__ m_out, float* __restrict__ l_out, int normalize, int n_src,
+             int n_q, int64_t n_tok, float eps, float inv_d) {
+  using M = Mx<T>;
+  constexpr int d = 128 * KS;
+  constexpr uint32_t rs = (uint32_t)d * 2u + kMxPad;  // LDS row stride (bytes)
+  constexpr uint32_t row_bytes = (uint32_t)d * 2u;
+  constexpr int cpr = 4 * KS;  // 16-byte chunks per row in a wave's slice (<= 64)
+  constexpr uint32_t kDrop = 0x80000000u;  // store offset past every resource
+  extern __shared__ __align__(16) char vs[];
+  __shared__ __align__(16) float xl[2][kMxWaves][64][4];  // logit partials, C layout
+  __shared__ __align__(16) float xs[2][kMxWaves][kMxRows];  // sum-of-squares partials
+  // Output staging: [query][kMxGroup * 32 columns] per wave, so that stores go
+  // out as 256-byte row segments (the MFMA result layout gives each lane 16
+  // bytes of one query, 64 contiguous bytes per query per instruction).
+  __shared__ __align__(16) char ob[kMxWaves][(int)kMatrixMaxQ][kMxGroup * 64];
+
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int qi = lane & 15;  // MFMA column: query (logits, output) / row (A of logits)
+  const int g = lane >> 4;   // 16-lane group
+  const int cb = w * 32 * KS;  // first column of this wave
+
+  // Query slice, B operand of the logits: Q[s][cb + 32k + 8g .. +7], s = qi
+  // (queries past n_q repeat the last one; their columns are never stored).
+  i32x4_t qr[KS];
+  {
+    const int sq = qi < n_q ? qi : n_q - 1;
+    const auto r = make_rsrc(q, (uint32_t)n_q * row_bytes);
+#pragma unroll
+    for (int k = 0; k < KS; ++k) qr[k] = ld16(r, (uint32_t)(sq * d + cb + 32 * k + 8 * g) * 2u);
+  }
+  // Zero row (index n_src), this wave's slice.
+  if (lane < cpr) *(i32x4_t*)(vs + n_src * rs + (cb + 8 * lane) * 2) = i32x4_t{0, 0, 0, 0};
+
+  const int64_t step = gridDim.x;
+  const int64_t first = blockIdx.x;
+  const int iters = first < n_tok ? (int)((n_tok - first + step - 1) / step) : 0;
+  if (iters == 0) return;  // uniform over the workgroup
+
+  // Staging: chunk `lane` of each row of this wave's slice of token t.
+  auto stage = [&](i32x4_t (&st)[NR], int64_t t) {
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      const bool real = n < n_src;
+      const auto r = make_rsrc(row_of<const uint16_t>(v, real ? n : 0) + t * d,
+                               real ? row_bytes : 0u);
+      st[n] = ld16_stream(r, (uint32_t)(cb + 8 * lane) * 2u);
+    }
+  };
+  auto commit = [&](const i32x4_t (&st)[NR]) {
+    wave_lds_fence();
+    if (lane < cpr) {
+#pragma unroll
+      for (int n = 0; n < NR; ++n)
+        if (n < n_src) *(i32x4_t*)(vs + n * rs + (cb + 8 * lane) * 2) = st[n];
+    }
+    wave_lds_fence();
+  };
+
+  // Row this lane feeds to the logits (A: row qi) and to the output product
+  // (A: the 4x4-transposed read supplies row 4g + qi/4); missing rows read the
+  // zero row.
+  const int ra = qi < n_src ? qi : n_src;
+  const int rt = 4 * g + (qi >> 2) < n_src ? 4 * g + (qi >> 2) : n_src;
+  const char* abase = vs + ra * rs + (cb + 8 * g) * 2;
+  const char* tbase = vs + rt * rs + (cb + 8 * (qi & 3)) * 2;
+  // Statistics: lanes 0..15 of wave 0 own query qi; others store out of range.
+  const bool stat_lane = w == 0 && g == 0 && qi < n_q;
+  const uint32_t stat_bytes = m_out != nullptr ? (uint32_t)((int64_t)n_q * n_tok * 4) : 0u;
+  // Output rounds: lane l stores query 4r + l/16, 16-byte chunk l%16 of the
+  // group; rows of a round are n_tok * d apart.
+  const uint32_t q_stride = (uint32_t)(n_tok * d * 2);
+
+  // One token whose rows are in LDS; k selects the exchange buffer.
+  auto token = [&](int k, int64_t tok) {
+    // Logit and sum-of-squares partials over this wave's columns.
+    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    float ss = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      const i32x4_t a = *(const i32x4_t*)(abase + kk * 64);
+      ss = dot<T>(a, a, ss);
+      acc = M::k32(a, qr[kk], acc);
+    }
+    ss += __shfl_xor(ss, 16);
+    ss += __shfl_xor(ss, 32);
+    const int xb = k & 1;
+    *(f32x4_t*)&xl[xb][w][lane][0] = acc;
+    if (lane < kMxRows) xs[xb][w][lane] = ss;
+    __syncthreads();
+    // Lane (g, qi) now holds rows n = 4g + j of query column s = qi.
+    f32x4_t lt = *(const f32x4_t*)&xl[xb][0][lane][0];
+    f32x4_t sq = *(const f32x4_t*)&xs[xb][0][4 * g];
+#pragma unroll
+    for (int ww = 1; ww < kMxWaves; ++ww) {
+      lt += *(const f32x4_t*)&xl[xb][ww][lane][0];
+      sq += *(const f32x4_t*)&xs[xb][ww][4 * g];
+    }
+
+    // Softmax over the rows of each query column (4 rows a lane, 4 lanes).
+    float lg[4], p[4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      lg[j] = 4 * g + j < n_src ? lt[j] * rsqrtf(fmaf(sq[j], inv_d, eps)) : -INFINITY;
+      mx = fmaxf(mx, lg[j]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    float ls = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      p[j] = 4 * g + j < n_src ? expf(lg[j] - mx) : 0.0f;
+      ls += p[j];
+    }
+    ls += __shfl_xor(ls, 16);
+    ls += __shfl_xor(ls, 32);
+
+    // B operand of the output product: P^T[4g + j][qi], high and low parts.
+    const int h01 = M::pack2(p[0], p[1]), h23 = M::pack2(p[2], p[3]);
+    const i32x2_t ph = {h01, h23};
+    const i32x2_t pl = {M::pack2(p[0] - M::lo(h01), p[1] - M::hi(h01)),
+                        M::pack2(p[2] - M::lo(h23), p[3] - M::hi(h23))};
+
+    // Output: blocks of 32 columns; the two 16-column MFMAs of a block
+    // interleave so that lane (g, qi) ends with columns 8g .. 8g+7 of query qi.
+    // Every kMxGroup blocks go through LDS and out as 256-byte row segments.
+    const float inv_l = normalize ? 1.0f / ls : 1.0f;
+    char* obw = &ob[w][0][0];
+#pragma unroll
+    for (int pi = 0; pi < KS; ++pi) {
+      const char* ap = tbase + pi * 64;
+      const i32x2_t a0 = __builtin_bit_cast(
+          i32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(ap)));
+      const i32x2_t a1 = __builtin_bit_cast(
+          i32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(ap + 8)));
+      f32x4_t c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = {0.0f, 0.0f, 0.0f, 0.0f};
+      c0 = M::k16(a0, pl, c0);
+      c1 = M::k16(a1, pl, c1);
+      c0 = M::k16(a0, ph, c0);
+      c1 = M::k16(a1, ph, c1);
+      float f[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f[j] = c0[j] * inv_l;
+        f[4 + j] = c1[j] * inv_l;
+      }
+      if (pi % kMxGroup == 0) wave_lds_fence();
+      *(i32x4_t*)(obw + qi * (kMxGroup * 64) + (pi % kMxGroup) * 64 + g * 16) = pack<T>(f);
+      if (pi % kMxGroup == kMxGroup - 1 || pi == KS - 1) {
+        wave_lds_fence();
+        const int pi0 = pi - pi % kMxGroup;
+        constexpr int kRounds = (int)kMatrixMaxQ / 4;
+#pragma unroll
+        for (int rr = 0; rr < kRounds; ++rr) {
+          const int s = 4 * rr + (lane >> 4);
+          const int ch = lane & 15;  // 16-byte chunk within the group
+          const i32x4_t val = *(const i32x4_t*)(obw + s * (kMxGroup * 64) + ch * 16);
+          const int live = n_q - 4 * rr;  // queries of this round (may be <= 0)
+          const uint32_t bytes =
+              live <= 0 ? 0u : (uint32_t)(live > 4 ? 3 : live - 1) * q_stride + row_bytes;
+          const auto orr =
+              make_rsrc(out + ((int64_t)(live > 0 ? 4 * rr : 0) * n_tok + tok) * d, bytes);
+          const bool ok = s < n_q && 8 * ch < 32 * (pi - pi0 + 1);
+          st16_stream(orr,
+                      ok ? (uint32_t)(lane >> 4) * q_stride + (uint32_t)(cb + 32 * pi0 + 8 * ch) * 2u
+                         : kDrop,
+                      val);
+        }
+      }
+    }
+    const auto mr = make_rsrc(m_out, stat_bytes);
+    const auto lr = make_rsrc(l_out, stat_bytes);
+    const uint32_t so = stat_lane ? (uint32_t)(((int64_t)qi * n_tok + tok) * 4) : kDrop;
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(mx), mr, so, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(ls), lr, so, 0, 0);
+  };
+
+  i32x4_t sa[NR], sb[NR];
+  stage(sa, first);
+  // Queries and the first token have landed before the loop: the compiler
+  // then knows no register of theirs is pending inside it.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  commit(sa);
+  if (iters > 1) stage(sb, first + step);
+  for (int k = 0; k < iters; k += 2) {
+    // Token k is in LDS, token k+1 in flight in sb.
+    const int64_t tok = first + (int64_t)k * step;
+    if (k + 2 < iters) stage(sa, tok + 2 * step);
+    token(k, tok);
+    if (k + 1 >= iters) break;
+    commit(sb);
+    if (k + 3 < iters) stage(sb, tok + 3 * step);
+    token(k + 1, tok + step);
+    if (k + 2 < iters) commit(sa);
+  }
+}
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+template <class T, int KS, int NR>
+hipError_t launch_mx(const BatchedArgs& a, hipStream_t s, KernelRes* info) {
+  const size_t lds = (size_t)(a.n_src + 1) * ((size_t)a.d * 2 + kMxPad);
+  auto* kern = k_batched_mx<T, KS, NR>;
+  KernelRes r{0, 0, 1, 0};
+  hipFuncAttributes fa;
+  hipError_t e = hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(kern));
+  if (e != hipSuccess) return e;
+  r.vgprs = fa.numRegs;
+  r.lds = (int)(fa.sharedSizeBytes + lds);
+  const int alloc = std::max(8, ((fa.numRegs + 7) / 8) * 8);
+  const int by_waves = std::min(8, 512 / alloc);  // one wave per SIMD per workgroup
+  r.blocks_per_cu = std::max(1, std::min(by_waves, (160 * 1024) / std::max(1, r.lds)));
+  int cus = 0;
+  if (cu_count(&cus) != hipSuccess || cus < 1) cus = 1;
+  r.grid = (int)std::max<int64_t>(1, std::min<int64_t>((int64_t)cus * r.blocks_per_cu, a.n_tok));
+  if (info != nullptr) {
+    *info = r;
+    return hipSuccess;
+  }
+  if (lds > 64 * 1024) {
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(kern, dim3(r.grid), dim3(64 * kMxWaves), lds, s, a.v, (const uint16_t*)a.q,
+                     (uint16_t*)a.out, a.m_out, a.l_out, a.normalize, a.n_src, a.n_q, a.n_tok,
+                     a.eps, 1.0f / (float)a.d);
+  return hipGetLastError();
+}
+
+template <class T, int KS>
+hipError_t launch_mx_rows(const BatchedArgs& a, hipStream_t s, KernelRes* info) {
+  return a.n_src <= 9 ? launch_mx<T, KS, 9>(a, s, info) : launch_mx<T, KS, 16>(a, s, info);
+}
+
+template <class T>
+hipError_t launch_mx_dtype(const BatchedArgs& a, hipStream_t s, KernelRes* info) {
+  switch (a.d / 128) {
+    case 4: return launch_mx_rows<T, 4>(a, s, info);
+    case 8: return launch_mx_rows<T, 8>(a, s, info);
+    case 12: return launch_mx_rows<T, 12>(a, s, info);
+    case 16: return launch_mx_rows<T, 16>(a, s, info);
+    default: return hipErrorInvalidConfiguration;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_batched_matrix(const BatchedArgs& a, hipStream_t s, KernelRes* info) {
+  if (!matrix_batched_fits(a.n_src, a.n_q, a.d, a.dtype)) return hipErrorInvalidConfiguration;
+  if (!matrix_batched_offsets_fit(a.n_q, a.n_tok, a.d)) return hipErrorInvalidConfiguration;
+  if (a.n_tok == 0) return hipSuccess;
+  return a.dtype == SY_BF16 ? launch_mx_dtype<BF16>(a, s, info) : launch_mx_dtype<F16>(a, s, info);
+}
+
+}  // namespace sy

@@ -22,7 +22,10 @@
 //     admits 16 rows x 2 chunks when the forward's stats are passed (that
 //     variant holds no recompute state and fits 256 VGPRs); without stats that
 //     tile spills and the thinner one is kept.
-//  5. Batched: resident with S <= 16, else one forward launch per query.
+//  5. Batched: 16-bit inputs with N <= 16, 6 <= S <= 16 and D in {512, 1024,
+//     1536, 2048} run on the matrix cores (config 3: 8 queries x 9 rows is ~7000
+//     VALU instructions a token on the register tile); otherwise resident with
+//     S <= 16, else one forward launch per query.
 //  6. Batched backward: one chunk per lane on the fewest waves that cover the
 //     row, N <= 9 and S <= 8 (dv and dq accumulators stay in registers);
 //     otherwise the generic kernel while its LDS scalars fit.
@@ -126,6 +129,17 @@ int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_
     return SY_OK;
   }
 
+  if (op == SY_OP_BATCHED && vec && matrix_batched_fits(n_src, n_q, d, v_dtype)) {
+    out->family = SY_FAMILY_MATRIX;
+    out->waves_per_token = 4;
+    out->chunks_per_lane = 1;
+    out->rows_per_tile = (int)kMatrixMaxRows;
+    out->elems_per_chunk = ce;
+    out->block_threads = 256;
+    out->tokens_per_block = 1;
+    out->n_chunks = 1;
+    return SY_OK;
+  }
   // Four chunks per lane at one wave per SIMD pay off from 5 rows on (N=9:
   // 62.2 vs 64.9 us); with N <= 4 two chunks on twice the waves are faster
   // (N=4: 36.4 vs 38.4 us, N=2: 24.6 vs 27.7 us). Eight waves of such a tile
@@ -200,7 +214,8 @@ bool tile_listed(int op, int w, int vpl, int nr) {
 // plan when that tile is built, covers the row, and (backward, batched) holds
 // every row. Anything else leaves the plan untouched.
 void apply_tile_override(int op, int64_t n_src, int64_t d, sy_plan* p) {
-  if (p->family != SY_FAMILY_RESIDENT && p->family != SY_FAMILY_CHUNKED) return;
+  const bool tiled = p->family == SY_FAMILY_RESIDENT || p->family == SY_FAMILY_CHUNKED;
+  if (!tiled && !(op == SY_OP_BATCHED && p->family == SY_FAMILY_MATRIX)) return;
   const char* name = op == SY_OP_FWD ? "SY_TILE_FWD"
                      : op == SY_OP_BWD ? "SY_TILE_BWD"
                      : op == SY_OP_BATCHED ? "SY_TILE_BATCHED"

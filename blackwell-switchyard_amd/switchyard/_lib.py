@@ -19,7 +19,7 @@ LIB_PATH = pathlib.Path(__file__).resolve().parent / "libswitchyard_hip.so"
 
 SY_F32, SY_F16, SY_BF16 = 0, 1, 2
 OP_FWD, OP_BWD, OP_BATCHED, OP_SOL, OP_BWD_BATCHED = 0, 1, 2, 3, 4
-FAMILY_NAMES = {0: "resident", 1: "chunked", 2: "generic", 3: "per_query"}
+FAMILY_NAMES = {0: "resident", 1: "chunked", 2: "generic", 3: "per_query", 4: "matrix"}
 
 _DTYPE_CODES = {torch.float32: SY_F32, torch.float16: SY_F16, torch.bfloat16: SY_BF16}
 

@@ -317,6 +317,9 @@ def _bwd_launch(n: int, d: int, dtype: torch.dtype = torch.bfloat16) -> tuple[bo
 
 
 def _batched_launch(n: int, d: int, s: int, dtype: torch.dtype = torch.bfloat16) -> tuple[bool, int, int, int]:
-    """Batched plan: ``(resident, waves_per_token, chunks_per_lane, rows_per_tile)``."""
+    """Batched plan: ``(one_kernel, waves_per_token, chunks_per_lane, rows_per_tile)``;
+    one_kernel is the reference's "resident" flag (one launch for all queries),
+    true for the register-tiled and the matrix-core kernels."""
     p = _lib.plan(_lib.OP_BATCHED, n, d, dtype, n_q=s)
-    return p["family_name"] == "resident", p["waves_per_token"], p["chunks_per_lane"], p["rows_per_tile"]
+    one = p["family_name"] in ("resident", "matrix")
+    return one, p["waves_per_token"], p["chunks_per_lane"], p["rows_per_tile"]

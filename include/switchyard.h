@@ -76,7 +76,9 @@ typedef enum sy_family {
   SY_FAMILY_RESIDENT = 0,  /* the whole [N, D] token tile lives in registers       */
   SY_FAMILY_CHUNKED = 1,   /* register tile of NR rows, online softmax over chunks */
   SY_FAMILY_GENERIC = 2,   /* element-wise loads, two passes per token             */
-  SY_FAMILY_PER_QUERY = 3  /* batched op answered by one forward launch per query  */
+  SY_FAMILY_PER_QUERY = 3, /* batched op answered by one forward launch per query  */
+  SY_FAMILY_MATRIX = 4     /* batched op on the matrix cores: 4 waves per token,
+                              [N, D] staged in LDS, queries in registers         */
 } sy_family;
 
 /* How a call will be executed: which kernel family and which compile-time tile.

@@ -173,7 +173,8 @@ def plan(op, n, d, dt=torch.bfloat16, **kw):
 def test_representative_shape_is_register_resident_everywhere():
     for op in (_lib.OP_FWD, _lib.OP_BWD, _lib.OP_SOL):
         assert plan(op, 9, 2048)["family_name"] == "resident"
-    assert plan(_lib.OP_BATCHED, 9, 2048, n_q=8)["family_name"] == "resident"
+    assert plan(_lib.OP_BATCHED, 9, 2048, n_q=8)["family_name"] == "matrix"
+    assert plan(_lib.OP_BATCHED, 9, 2048, torch.float32, n_q=8)["family_name"] == "resident"
 
 
 @pytest.mark.parametrize("n,d", [(9, 4096), (16, 2048), (9, 8192), (16, 4096), (4, 1024), (1, 256)])
@@ -222,8 +223,28 @@ def test_unaligned_rows_and_mixed_dtypes_take_the_generic_kernels():
 
 
 def test_batched_query_cap():
-    assert plan(_lib.OP_BATCHED, 9, 2048, n_q=16)["family_name"] == "resident"
+    assert plan(_lib.OP_BATCHED, 9, 2048, n_q=16)["family_name"] == "matrix"
+    assert plan(_lib.OP_BATCHED, 9, 2048, torch.float32, n_q=16)["family_name"] == "resident"
     assert plan(_lib.OP_BATCHED, 9, 2048, n_q=17)["family_name"] == "per_query"
+
+
+def test_batched_matrix_core_plan_bounds():
+    """16-bit inputs with N <= 16, S <= 16 and D in {512, 1024, 1536, 2048}
+    take the matrix-core kernel; anything else keeps the register tiles."""
+    fam = lambda n, d, s, dt=torch.bfloat16: plan(_lib.OP_BATCHED, n, d, dt, n_q=s)["family_name"]
+    for dt in (torch.bfloat16, torch.float16):
+        for d in (512, 1024, 1536, 2048):
+            assert fam(1, d, 6, dt) == "matrix"
+            assert fam(16, d, 16, dt) == "matrix"
+    assert fam(9, 2048, 5) == "resident"  # few queries: the register tile is faster
+    assert fam(17, 2048, 8) != "matrix"
+    assert fam(9, 4096, 8) == "resident"
+    assert fam(9, 256, 8) == "resident"
+    assert fam(9, 1000, 8) != "matrix"
+    assert fam(9, 2048, 8, torch.float32) == "resident"
+    assert plan(_lib.OP_BATCHED, 9, 2048, n_q=8, aligned=False)["family_name"] == "per_query"
+    p = plan(_lib.OP_BATCHED, 9, 2048, n_q=8)
+    assert (p["waves_per_token"], p["block_threads"], p["tokens_per_block"]) == (4, 256, 1)
 
 
 def test_backward_takes_four_chunks_only_with_one_wave_per_simd():

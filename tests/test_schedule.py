@@ -226,6 +226,29 @@ def test_batched_with_stats(nsd, dtype):
     assert out.shape == o.shape
 
 
+@pytest.mark.parametrize("nstd", [(9, 8, 1100, 2048), (16, 16, 517, 2048), (1, 6, 300, 512),
+                                  (12, 13, 777, 1536), (5, 7, 1025, 1024)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_batched_matrix_kernel(nstd, dtype):
+    """The matrix-core batched forward (6..16 queries, 16-bit inputs): outputs
+    and statistics against the C oracle over token counts that run the
+    persistent loop an odd and an even number of times per workgroup."""
+    n, s, t, d = nstd
+    assert _lib.plan(_lib.OP_BATCHED, n, d, dtype, n_q=s)["family_name"] == "matrix"
+    print(f"matrix batched {nstd} {dtype}", flush=True)
+    v, _ = _make(n, t, d, dtype, seed=21)
+    q = (torch.randn(s, d, generator=torch.Generator().manual_seed(22)) * 0.5).to(dtype).to(DEV)
+    with torch.no_grad():
+        o, m, ell = block_attn_res_batched_with_stats(v, q)
+        out = block_attn_res_batched(v, q)
+    _close(out[:, 0].cpu(), c_oracle.batched(_np(v)[:, 0], _np(q)), dtype, what="out")
+    for k in range(s):
+        ro, rm, rl = c_oracle.attn_with_stats(_np(v)[:, 0], _np(q)[k])
+        _close(o[k, 0].cpu(), ro, dtype, what=f"o[{k}]")
+        _stat_close(m[k, 0].cpu(), rm, f"m[{k}]")
+        _stat_close(ell[k, 0].cpu(), rl, f"l[{k}]")
+
+
 # -- batched backward --------------------------------------------------------
 
 
