@@ -47,8 +47,19 @@ typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 
 constexpr int kMxWaves = 4;                               // waves per workgroup, one token
 constexpr int kMxRows = (int)kMatrixMaxRows;              // MFMA M of the logits, K of the output
-constexpr int kMxPad = 64;                                // LDS row padding (bytes)
-constexpr int kMxGroup = 4;  // 32-column output blocks staged in LDS per store round
+// LDS layouts (32 banks of 4 bytes):
+//  * source rows: stride = D*2 + 16 bytes, so the 8 rows one 16-byte read
+//    pass of the logits touches (same column, rows qi) fall in 8 different
+//    4-bank groups;
+//  * transposed reads: within each 64-column block, output MFMA a takes from
+//    lane (row r = q/4, piece c = q%4) the 8 bytes at 16a + 8(c%2) + 64(c/2):
+//    with the 16-byte row skew, the 16 lanes of a pass cover 16 distinct
+//    2-bank pairs;
+//  * output staging: SC columns per query row (256 with at most 8 queries,
+//    else 128), stride SC*2 + 16 bytes, written 8 bytes a lane (2-way bank
+//    conflicts), read back as contiguous 16-byte chunks so that each store
+//    instruction writes SC*2-byte segments of 64*16/(SC*2) query rows.
+constexpr int kMxPad = 16;  // source-row skew (bytes)
 
 template <class T> struct Mx;
 template <> struct Mx<BF16> {
@@ -109,7 +120,7 @@ __device__ __forceinline__ void wave_lds_fence() {
 // theirs), so the number of memory operations between a prefetch and its use
 // is a compile-time constant and the compiler waits for exactly the prefetch,
 // not for everything in flight.
-template <class T, int KS, int NR>
+template <class T, int KS, int NR, int SQ>
 __global__ void __launch_bounds__(256, 2)
 k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restrict__ out,
              float* __restrict__ m_out, float* __restrict__ l_out, int normalize, int n_src,
@@ -123,10 +134,17 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
   extern __shared__ __align__(16) char vs[];
   __shared__ __align__(16) float xl[2][kMxWaves][64][4];  // logit partials, C layout
   __shared__ __align__(16) float xs[2][kMxWaves][kMxRows];  // sum-of-squares partials
-  // Output staging: [query][kMxGroup * 32 columns] per wave, so that stores go
-  // out as 256-byte row segments (the MFMA result layout gives each lane 16
-  // bytes of one query, 64 contiguous bytes per query per instruction).
-  __shared__ __align__(16) char ob[kMxWaves][(int)kMatrixMaxQ][kMxGroup * 64];
+  // Output staging: [query][SC columns] per wave (the MFMA result layout
+  // gives each lane 8 bytes of one query).
+  // 256-column rounds halve the store count; the 16-row staging leaves no
+  // registers for their wider operand window.
+  constexpr int SC = SQ <= 8 && KS % 8 == 0 && NR <= 9 ? 256 : 128;  // columns per round
+  static_assert((32 * KS) % SC == 0, "store rounds must tile the wave's columns");
+  constexpr int kRow = SC * 2 + 16;                   // staging row stride (bytes)
+  constexpr int kLpq = SC / 8;                        // lanes per query row
+  constexpr int kQpi = 64 / kLpq;                     // query rows per store
+  constexpr int kRounds = SQ / kQpi;
+  __shared__ __align__(16) char ob[kMxWaves][SQ * kRow];
 
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
@@ -151,12 +169,15 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
   const int iters = first < n_tok ? (int)((n_tok - first + step - 1) / step) : 0;
   if (iters == 0) return;  // uniform over the workgroup
 
-  // Staging: chunk `lane` of each row of this wave's slice of token t.
+  // Staging: chunk `lane` of each row of this wave's slice of token t (rows
+  // past n_src and tokens past n_tok load zeros through a zero-size resource).
   auto stage = [&](i32x4_t (&st)[NR], int64_t t) {
+    const bool tok_ok = t < n_tok;
+    const int64_t tc = tok_ok ? t : n_tok - 1;
 #pragma unroll
     for (int n = 0; n < NR; ++n) {
-      const bool real = n < n_src;
-      const auto r = make_rsrc(row_of<const uint16_t>(v, real ? n : 0) + t * d,
+      const bool real = n < n_src && tok_ok;
+      const auto r = make_rsrc(row_of<const uint16_t>(v, n < n_src ? n : 0) + tc * d,
                                real ? row_bytes : 0u);
       st[n] = ld16_stream(r, (uint32_t)(cb + 8 * lane) * 2u);
     }
@@ -177,7 +198,7 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
   const int ra = qi < n_src ? qi : n_src;
   const int rt = 4 * g + (qi >> 2) < n_src ? 4 * g + (qi >> 2) : n_src;
   const char* abase = vs + ra * rs + (cb + 8 * g) * 2;
-  const char* tbase = vs + rt * rs + (cb + 8 * (qi & 3)) * 2;
+  const char* tbase = vs + rt * rs + cb * 2 + 8 * (qi & 1) + 64 * ((qi >> 1) & 1);
   // Statistics: lanes 0..15 of wave 0 own query qi; others store out of range.
   const bool stat_lane = w == 0 && g == 0 && qi < n_q;
   const uint32_t stat_bytes = m_out != nullptr ? (uint32_t)((int64_t)n_q * n_tok * 4) : 0u;
@@ -187,15 +208,29 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
 
   // One token whose rows are in LDS; k selects the exchange buffer.
   auto token = [&](int k, int64_t tok) {
-    // Logit and sum-of-squares partials over this wave's columns.
-    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    float ss = 0.0f;
+    // Logit and sum-of-squares partials over this wave's columns: row chunks
+    // are read kAhead steps ahead of their MFMA, and even and odd steps
+    // accumulate in separate chains.
+    constexpr int kAhead = 4;
+    f32x4_t acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+    float ss0 = 0.0f, ss1 = 0.0f;
+    i32x4_t win[kAhead];
+#pragma unroll
+    for (int kk = 0; kk < kAhead && kk < KS; ++kk) win[kk] = *(const i32x4_t*)(abase + kk * 64);
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
-      const i32x4_t a = *(const i32x4_t*)(abase + kk * 64);
-      ss = dot<T>(a, a, ss);
-      acc = M::k32(a, qr[kk], acc);
+      const i32x4_t a = win[kk % kAhead];
+      if (kk + kAhead < KS) win[kk % kAhead] = *(const i32x4_t*)(abase + (kk + kAhead) * 64);
+      if (kk % 2 == 0) {
+        ss0 = dot<T>(a, a, ss0);
+        acc0 = M::k32(a, qr[kk], acc0);
+      } else {
+        ss1 = dot<T>(a, a, ss1);
+        acc1 = M::k32(a, qr[kk], acc1);
+      }
     }
+    const f32x4_t acc = acc0 + acc1;
+    float ss = ss0 + ss1;
     ss += __shfl_xor(ss, 16);
     ss += __shfl_xor(ss, 32);
     const int xb = k & 1;
@@ -203,12 +238,17 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
     if (lane < kMxRows) xs[xb][w][lane] = ss;
     __syncthreads();
     // Lane (g, qi) now holds rows n = 4g + j of query column s = qi.
-    f32x4_t lt = *(const f32x4_t*)&xl[xb][0][lane][0];
-    f32x4_t sq = *(const f32x4_t*)&xs[xb][0][4 * g];
+    f32x4_t pl4[kMxWaves], ps4[kMxWaves];
+#pragma unroll
+    for (int ww = 0; ww < kMxWaves; ++ww) {
+      pl4[ww] = *(const f32x4_t*)&xl[xb][ww][lane][0];
+      ps4[ww] = *(const f32x4_t*)&xs[xb][ww][4 * g];
+    }
+    f32x4_t lt = pl4[0], sq = ps4[0];
 #pragma unroll
     for (int ww = 1; ww < kMxWaves; ++ww) {
-      lt += *(const f32x4_t*)&xl[xb][ww][lane][0];
-      sq += *(const f32x4_t*)&xs[xb][ww][4 * g];
+      lt += pl4[ww];
+      sq += ps4[ww];
     }
 
     // Softmax over the rows of each query column (4 rows a lane, 4 lanes).
@@ -236,50 +276,63 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
     const i32x2_t pl = {M::pack2(p[0] - M::lo(h01), p[1] - M::hi(h01)),
                         M::pack2(p[2] - M::lo(h23), p[3] - M::hi(h23))};
 
-    // Output: blocks of 32 columns; the two 16-column MFMAs of a block
-    // interleave so that lane (g, qi) ends with columns 8g .. 8g+7 of query qi.
-    // Every kMxGroup blocks go through LDS and out as 256-byte row segments.
+    // Output, 64 columns at a time (4 MFMA pairs, high and low weight parts).
+    // Lane (g, qi) of MFMA a holds query qi at local columns
+    // 8a + 4(g%2) + 32(g/2) + j, j < 4; it stages them (8 bytes) and every
+    // SC columns the wave stores SC*2-byte row segments.
     const float inv_l = normalize ? 1.0f / ls : 1.0f;
-    char* obw = &ob[w][0][0];
+    char* obw = ob[w];
+    constexpr int kBlocks = KS / 2;            // 64-column blocks of this wave
+    constexpr int kPerStage = SC / 64;         // blocks per store round
+    auto tread = [&](int b, int a) {
+      return __builtin_bit_cast(i32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                             (lds_s16x4_t*)(tbase + b * 128 + a * 16)));
+    };
+    const int ocol = 4 * (g & 1) + 32 * (g >> 1);  // lane's first local column
+    i32x2_t tw[kPerStage][4];
 #pragma unroll
-    for (int pi = 0; pi < KS; ++pi) {
-      const char* ap = tbase + pi * 64;
-      const i32x2_t a0 = __builtin_bit_cast(
-          i32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(ap)));
-      const i32x2_t a1 = __builtin_bit_cast(
-          i32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(ap + 8)));
-      f32x4_t c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = {0.0f, 0.0f, 0.0f, 0.0f};
-      c0 = M::k16(a0, pl, c0);
-      c1 = M::k16(a1, pl, c1);
-      c0 = M::k16(a0, ph, c0);
-      c1 = M::k16(a1, ph, c1);
-      float f[8];
+    for (int j = 0; j < kPerStage; ++j)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        f[j] = c0[j] * inv_l;
-        f[4 + j] = c1[j] * inv_l;
+      for (int a = 0; a < 4; ++a) tw[j][a] = tread(j, a);
+#pragma unroll
+    for (int b = 0; b < kBlocks; ++b) {
+      if (b % kPerStage == 0) wave_lds_fence();
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        f32x4_t c = {0.0f, 0.0f, 0.0f, 0.0f};
+        c = M::k16(tw[b % kPerStage][a], pl, c);
+        c = M::k16(tw[b % kPerStage][a], ph, c);
+        const i32x2_t o = {M::pack2(c[0] * inv_l, c[1] * inv_l),
+                           M::pack2(c[2] * inv_l, c[3] * inv_l)};
+        if (qi < SQ) *(i32x2_t*)(obw + qi * kRow + ((b % kPerStage) * 64 + 8 * a + ocol) * 2) = o;
       }
-      if (pi % kMxGroup == 0) wave_lds_fence();
-      *(i32x4_t*)(obw + qi * (kMxGroup * 64) + (pi % kMxGroup) * 64 + g * 16) = pack<T>(f);
-      if (pi % kMxGroup == kMxGroup - 1 || pi == KS - 1) {
+      if (b % kPerStage == kPerStage - 1) {
+        // Next round's operands go out before the staging round trip.
+#pragma unroll
+        for (int j = 0; j < kPerStage; ++j)
+          if (b + 1 + j < kBlocks)
+#pragma unroll
+            for (int a = 0; a < 4; ++a) tw[j][a] = tread(b + 1 + j, a);
         wave_lds_fence();
-        const int pi0 = pi - pi % kMxGroup;
-        constexpr int kRounds = (int)kMatrixMaxQ / 4;
+        const int col0 = cb + 64 * (b + 1 - kPerStage);  // first column of the round
+        const int chunk = lane % kLpq;  // 16-byte chunk of a query's segment
+        i32x4_t vals[kRounds];
+#pragma unroll
+        for (int rr = 0; rr < kRounds; ++rr)
+          vals[rr] = *(const i32x4_t*)(obw + (kQpi * rr + lane / kLpq) * kRow + chunk * 16);
 #pragma unroll
         for (int rr = 0; rr < kRounds; ++rr) {
-          const int s = 4 * rr + (lane >> 4);
-          const int ch = lane & 15;  // 16-byte chunk within the group
-          const i32x4_t val = *(const i32x4_t*)(obw + s * (kMxGroup * 64) + ch * 16);
-          const int live = n_q - 4 * rr;  // queries of this round (may be <= 0)
+          const int live = n_q - kQpi * rr;  // queries of this round (may be <= 0)
           const uint32_t bytes =
-              live <= 0 ? 0u : (uint32_t)(live > 4 ? 3 : live - 1) * q_stride + row_bytes;
+              live <= 0 ? 0u
+                        : (uint32_t)(live > kQpi ? kQpi - 1 : live - 1) * q_stride + row_bytes;
           const auto orr =
-              make_rsrc(out + ((int64_t)(live > 0 ? 4 * rr : 0) * n_tok + tok) * d, bytes);
-          const bool ok = s < n_q && 8 * ch < 32 * (pi - pi0 + 1);
+              make_rsrc(out + ((int64_t)(live > 0 ? kQpi * rr : 0) * n_tok + tok) * d, bytes);
+          const bool ok = kQpi * rr + lane / kLpq < n_q;
           st16_stream(orr,
-                      ok ? (uint32_t)(lane >> 4) * q_stride + (uint32_t)(cb + 32 * pi0 + 8 * ch) * 2u
+                      ok ? (uint32_t)(lane / kLpq) * q_stride + (uint32_t)(col0 + 8 * chunk) * 2u
                          : kDrop,
-                      val);
+                      vals[rr]);
         }
       }
     }
@@ -290,32 +343,58 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
     __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(ls), lr, so, 0, 0);
   };
 
-  i32x4_t sa[NR], sb[NR];
+  // Stores one token issues (output rounds, then m and l).
+  constexpr int kTokenStores = (32 * KS / SC) * kRounds + 2;
+  // Two staged tokens in flight, except where 16 rows x 2048 columns would
+  // not leave the registers for two staging sets.
+  constexpr bool kTwoDeep = NR <= 9 || KS < 16;
+  i32x4_t sa[NR], sb[kTwoDeep ? NR : 1];
   stage(sa, first);
   // Queries and the first token have landed before the loop: the compiler
   // then knows no register of theirs is pending inside it.
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   commit(sa);
-  if (iters > 1) stage(sb, first + step);
-  for (int k = 0; k < iters; k += 2) {
-    // Token k is in LDS, token k+1 in flight in sb.
-    const int64_t tok = first + (int64_t)k * step;
-    if (k + 2 < iters) stage(sa, tok + 2 * step);
-    token(k, tok);
-    if (k + 1 >= iters) break;
-    commit(sb);
-    if (k + 3 < iters) stage(sb, tok + 3 * step);
-    token(k + 1, tok + step);
-    if (k + 2 < iters) commit(sa);
+  if constexpr (kTwoDeep) {
+    stage(sb, first + step);
+    // As many (dropped) stores as a token issues: entering the loop, the
+    // loads of sb are then followed by the same number of memory operations
+    // as on every later pass, so the compiler's wait before committing sb
+    // counts exactly those loads instead of also draining the previous
+    // token's stores. The scheduling barriers keep the stores after the loads.
+    __builtin_amdgcn_sched_barrier(0);
+    {
+      const auto none = make_rsrc(out, 0u);
+#pragma unroll
+      for (int i = 0; i < kTokenStores; ++i) st16_stream(none, 16u * i, i32x4_t{0, 0, 0, 0});
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    for (int k = 0; k < iters; k += 2) {
+      // Token k is in LDS, token k+1 in flight in sb.
+      const int64_t tok = first + (int64_t)k * step;
+      stage(sa, tok + 2 * step);
+      token(k, tok);
+      if (k + 1 >= iters) break;
+      commit(sb);
+      stage(sb, tok + 3 * step);
+      token(k + 1, tok + step);
+      if (k + 2 < iters) commit(sa);
+    }
+  } else {
+    for (int k = 0; k < iters; ++k) {
+      const int64_t tok = first + (int64_t)k * step;
+      stage(sa, tok + step);
+      token(k, tok);
+      if (k + 1 < iters) commit(sa);
+    }
   }
 }
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-template <class T, int KS, int NR>
+template <class T, int KS, int NR, int SQ>
 hipError_t launch_mx(const BatchedArgs& a, hipStream_t s, KernelRes* info) {
   const size_t lds = (size_t)(a.n_src + 1) * ((size_t)a.d * 2 + kMxPad);
-  auto* kern = k_batched_mx<T, KS, NR>;
+  auto* kern = k_batched_mx<T, KS, NR, SQ>;
   KernelRes r{0, 0, 1, 0};
   hipFuncAttributes fa;
   hipError_t e = hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(kern));
@@ -345,7 +424,9 @@ hipError_t launch_mx(const BatchedArgs& a, hipStream_t s, KernelRes* info) {
 
 template <class T, int KS>
 hipError_t launch_mx_rows(const BatchedArgs& a, hipStream_t s, KernelRes* info) {
-  return a.n_src <= 9 ? launch_mx<T, KS, 9>(a, s, info) : launch_mx<T, KS, 16>(a, s, info);
+  if (a.n_q <= 8)
+    return a.n_src <= 9 ? launch_mx<T, KS, 9, 8>(a, s, info) : launch_mx<T, KS, 16, 8>(a, s, info);
+  return a.n_src <= 9 ? launch_mx<T, KS, 9, 16>(a, s, info) : launch_mx<T, KS, 16, 16>(a, s, info);
 }
 
 template <class T>
