@@ -396,8 +396,11 @@ hipError_t launch_mx(const BatchedArgs& a, hipStream_t s, KernelRes* info) {
   const size_t lds = (size_t)(a.n_src + 1) * ((size_t)a.d * 2 + kMxPad);
   auto* kern = k_batched_mx<T, KS, NR, SQ>;
   KernelRes r{0, 0, 1, 0};
-  hipFuncAttributes fa;
-  hipError_t e = hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(kern));
+  // The attributes of an instantiation do not change: query them once.
+  static hipFuncAttributes fa;
+  static const hipError_t fa_err =
+      hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(kern));
+  hipError_t e = fa_err;
   if (e != hipSuccess) return e;
   r.vgprs = fa.numRegs;
   r.lds = (int)(fa.sharedSizeBytes + lds);
