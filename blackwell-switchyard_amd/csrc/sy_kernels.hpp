@@ -471,14 +471,17 @@ k_fwd_res(const RowTable v, const typename T::storage* __restrict__ w,
       }
     }
     if (live) {
-      if (stats != nullptr && seg == 0 && lane == 0) {
+      if (stats != nullptr && seg == 0) {
+        // One store instruction for the token's 2N statistics (lane i < N the
+        // logit of row i, lane 32 + i its r) instead of 2N single-lane ones.
+        float sv = 0.0f;
 #pragma unroll
         for (int n = 0; n < NR; ++n) {
-          if (n < rows) {
-            stats[(int64_t)n * n_tok + tok] = lg[n];
-            stats[(int64_t)(n_src + n) * n_tok + tok] = part[n];
-          }
+          sv = lane == n ? lg[n] : sv;
+          sv = lane == 32 + n ? part[n] : sv;
         }
+        const int i = lane & 31;
+        if (i < rows) stats[(int64_t)((lane >> 5) * n_src + i) * n_tok + tok] = sv;
       }
       if (m_out != nullptr && seg == 0 && lane == 0) {
         m_out[tok] = m;
