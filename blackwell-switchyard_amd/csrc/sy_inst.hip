@@ -181,10 +181,11 @@ hipError_t SY_FN(launch_bwd_vec_)(const sy_plan& p, const BwdArgs& a, int grid, 
 #define SY_BB_TILES(X) X(1, 4) X(1, 9) X(2, 4) X(2, 9) X(4, 4) X(4, 9) X(8, 4) X(8, 9)
 
 hipError_t SY_FN(bwd_batched_vec_resources_)(const sy_plan& p, KernelRes* out) {
+  // Sized by the variant with a runtime row count (the larger footprint).
 #define X(W_, N_)                                                                             \
   if (tile_is(p, W_, 1, N_)) {                                                                \
-    static const KernelRes kr =                                                               \
-        resources_of(k_bwd_batched<T, W_, N_, (int)kBwdBatchedMaxQ>, FwdGeom<W_>::kBlock);     \
+    static const KernelRes kr = resources_of(                                                 \
+        k_bwd_batched<T, W_, N_, (int)kBwdBatchedMaxQ, false>, FwdGeom<W_>::kBlock);            \
     *out = kr;                                                                                \
     return hipSuccess;                                                                        \
   }
@@ -197,15 +198,19 @@ hipError_t SY_FN(launch_bwd_batched_vec_)(const sy_plan& p, const BwdBatchedArgs
                                          hipStream_t s) {
   const float inv_d = 1.0f / (float)a.d;
   const int n_iter = (int)cdiv(a.n_tok, (int64_t)grid * p.tokens_per_block);
+#define SY_BB_LAUNCH(W_, N_, EX_)                                                             \
+  hipLaunchKernelGGL((k_bwd_batched<T, W_, N_, (int)kBwdBatchedMaxQ, EX_>), dim3(grid),       \
+                     dim3(FwdGeom<W_>::kBlock), 0, s, a.v, (const St*)a.q, (const St*)a.g,    \
+                     a.dv, a.partial, a.n_src, a.n_q, a.n_tok, a.d, a.eps, inv_d, n_iter)
 #define X(W_, N_)                                                                             \
   if (tile_is(p, W_, 1, N_)) {                                                                \
-    hipLaunchKernelGGL((k_bwd_batched<T, W_, N_, (int)kBwdBatchedMaxQ>), dim3(grid),           \
-                       dim3(FwdGeom<W_>::kBlock), 0, s, a.v, (const St*)a.q, (const St*)a.g,  \
-                       a.dv, a.partial, a.n_src, a.n_q, a.n_tok, a.d, a.eps, inv_d, n_iter);  \
+    if (a.n_src == N_) SY_BB_LAUNCH(W_, N_, true);                                            \
+    else SY_BB_LAUNCH(W_, N_, false);                                                         \
     return hipGetLastError();                                                                 \
   }
   SY_BB_TILES(X)
 #undef X
+#undef SY_BB_LAUNCH
   return hipErrorInvalidConfiguration;
 }
 

@@ -871,7 +871,10 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
 // One token per W waves with one chunk per lane (VPL = 1), persistent and
 // pipelined like k_bwd. Reference: the batched forward is
 // src/switchyard/triton_op.py:378-501; it has no backward.
-template <class T, int W, int NR, int SQ>
+// EXACT: n_src == NR, so every per-row guard is a compile-time constant (with
+// a runtime row count each of the ~18 guarded blocks per query becomes a
+// branch, and the merges cost register moves).
+template <class T, int W, int NR, int SQ, bool EXACT>
 __global__ void __launch_bounds__(FwdGeom<W>::kBlock)
 k_bwd_batched(const RowTable v, const typename T::storage* __restrict__ q,
               const typename T::storage* __restrict__ g, const RowTable dv,
@@ -896,7 +899,7 @@ k_bwd_batched(const RowTable v, const typename T::storage* __restrict__ q,
   const uint32_t lane_off = (uint32_t)(seg * 64 + lane) * 16u;
   const int64_t slots = (int64_t)gridDim.x * TPB;
   const int64_t first = (int64_t)blockIdx.x * TPB + slot;
-  const int rows = n_src;  // host guarantees n_src <= NR and n_q <= SQ
+  const int rows = EXACT ? NR : n_src;  // host guarantees n_src <= NR and n_q <= SQ
   int iters = n_iter;
   if constexpr (W == 1) iters = first < n_tok ? (int)((n_tok - first + slots - 1) / slots) : 0;
 
