@@ -63,11 +63,35 @@ int bwd_grid(const sy_plan& p, int64_t n_tok, int dtype, bool stats, int variant
   return SY_OK;
 }
 
+// Plan of the batched backward for this token count: the matrix-core kernel
+// only where its dv offsets fit.
+int bwd_batched_plan(int64_t n_src, int64_t n_q, int64_t n_tok, int64_t d, int dtype, int aligned,
+                     sy_plan* p) {
+  int rc = make_plan(SY_OP_BWD_BATCHED, n_src, n_q, d, dtype, dtype, aligned, p);
+  if (rc == SY_OK && p->family == SY_FAMILY_MATRIX && !bwd_matrix_offsets_fit(n_src, n_tok, d))
+    rc = make_plan(SY_OP_BWD_BATCHED, n_src, n_q, d, dtype, dtype, aligned, p, 1, 0);
+  return rc;
+}
+
 // Persistent grid of the batched backward (also sizes its workspace).
-int bwd_batched_grid(const sy_plan& p, int64_t n_tok, int dtype, int* grid) {
+int bwd_batched_grid(const sy_plan& p, int64_t n_src, int64_t n_q, int64_t n_tok, int64_t d,
+                     int dtype, int* grid) {
   int cus = 0;
   hipError_t e = cu_count(&cus);
   if (e != hipSuccess) return e == hipErrorNoDevice ? SY_ERR_DEVICE : (int)e;
+  if (p.family == SY_FAMILY_MATRIX) {
+    BwdBatchedArgs a{};
+    a.n_src = (int)n_src;
+    a.n_q = (int)n_q;
+    a.n_tok = n_tok;
+    a.d = (int)d;
+    a.dtype = dtype;
+    KernelRes r;
+    e = launch_bwd_batched_matrix(a, 0, nullptr, &r);
+    if (e != hipSuccess) return (int)e;
+    *grid = r.grid;
+    return SY_OK;
+  }
   int per_cu = 2;
   if (p.family != SY_FAMILY_GENERIC) {
     KernelRes r;
@@ -554,10 +578,10 @@ int64_t sy_bwd_batched_workspace_bytes(int64_t n_src, int64_t n_q, int64_t n_tok
   int64_t g = 0;
   for (int aligned : {1, 0}) {
     sy_plan p;
-    rc = make_plan(SY_OP_BWD_BATCHED, n_src, n_q, d, dtype, dtype, aligned, &p);
+    rc = bwd_batched_plan(n_src, n_q, n_tok, d, dtype, aligned, &p);
     if (rc != SY_OK) return rc;
     int gi = 0;
-    rc = bwd_batched_grid(p, n_tok, dtype, &gi);
+    rc = bwd_batched_grid(p, n_src, n_q, n_tok, d, dtype, &gi);
     if (rc != SY_OK) return rc;
     if (gi > g) g = gi;
   }
@@ -582,11 +606,11 @@ int sy_bwd_batched(const void* v, const void* queries, const void* grad_out, voi
   const bool aligned = vec_rows(vok && dok, d, dtype) && al16(queries) && al16(grad_out) &&
                        al16(workspace);
   sy_plan p;
-  rc = make_plan(SY_OP_BWD_BATCHED, n_src, n_q, d, dtype, dtype, aligned, &p);
+  rc = bwd_batched_plan(n_src, n_q, n_tok, d, dtype, aligned, &p);
   if (rc != SY_OK) return rc;
   int grid = 0;
   if (n_tok != 0) {
-    rc = bwd_batched_grid(p, n_tok, dtype, &grid);
+    rc = bwd_batched_grid(p, n_src, n_q, n_tok, d, dtype, &grid);
     if (rc != SY_OK) return rc;
     if (workspace == nullptr || workspace_bytes < (int64_t)grid * n_q * d * (int64_t)sizeof(float))
       return SY_ERR_WORKSPACE;
@@ -596,6 +620,8 @@ int sy_bwd_batched(const void* v, const void* queries, const void* grad_out, voi
     hipError_t e;
     if (p.family == SY_FAMILY_GENERIC) {
       e = launch_bwd_batched_generic(a, grid, s);
+    } else if (p.family == SY_FAMILY_MATRIX) {
+      e = launch_bwd_batched_matrix(a, grid, s, nullptr);
     } else {
       e = dtype == SY_BF16 ? launch_bwd_batched_vec_bf16(p, a, grid, s)
           : dtype == SY_F16 ? launch_bwd_batched_vec_f16(p, a, grid, s)

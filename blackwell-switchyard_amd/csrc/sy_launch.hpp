@@ -48,6 +48,35 @@ inline bool matrix_batched_fits(int64_t n_src, int64_t n_q, int64_t d, int dtype
 inline bool matrix_batched_offsets_fit(int64_t n_q, int64_t n_tok, int64_t d) {
   return 4 * n_tok * d * 2 < ((int64_t)1 << 31) && n_q * n_tok * 4 < ((int64_t)1 << 31);
 }
+// Batched backward on the matrix cores (sy_matrix.hip): 16-bit inputs, at most
+// 8 queries (g and the queries share the 16 columns of one MFMA tile), D in
+// {512, 1024, 1536, 2048}, and the workgroup's LDS within 160 KiB: 16 rows of
+// g and queries, the source rows and a zero row (dynamic), plus the logit
+// exchange, the coefficient tables and the dv staging (static, the kernel's
+// own arithmetic: 9 or 16 staged rows, 256- or 128-column store rounds).
+// The 16-row tile at D = 2048 would spill registers: there N <= 9.
+// Its dv stores address all source rows of a token from one buffer resource:
+// (n_src - 1) * n_tok * D * 2 + D * 2 bytes must stay below 2^31.
+constexpr int64_t kBwdMatrixMaxQ = 8;
+inline int64_t bwd_matrix_dynamic_lds(int64_t n_src, int64_t d) {
+  return (16 + n_src + 1) * (d * 2 + 16);
+}
+inline int64_t bwd_matrix_lds(int64_t n_src, int64_t d) {
+  const int64_t nr = n_src <= 9 ? 9 : 16;
+  const int64_t sc = nr <= 9 && (d / 128) % 8 == 0 ? 256 : 128;
+  const int64_t rows_per_store = 64 / (sc / 8);
+  const int64_t staged = (nr + rows_per_store - 1) / rows_per_store * rows_per_store;
+  const int64_t fixed = 2 * 4 * 64 * 16 + 2 * 4 * 16 * 4 + 4 * 16 * 20 * 4 + 4 * staged * (sc * 2 + 16);
+  return fixed + bwd_matrix_dynamic_lds(n_src, d);
+}
+inline bool bwd_matrix_fits(int64_t n_src, int64_t n_q, int64_t d, int dtype) {
+  return (dtype == SY_BF16 || dtype == SY_F16) && n_src >= 1 && n_src <= kMatrixMaxRows &&
+         n_q >= 1 && n_q <= kBwdMatrixMaxQ && (d == 512 || d == 1024 || d == 1536 || d == 2048) &&
+         (n_src <= 9 || d < 2048) && bwd_matrix_lds(n_src, d) <= 160 * 1024;
+}
+inline bool bwd_matrix_offsets_fit(int64_t n_src, int64_t n_tok, int64_t d) {
+  return (n_src - 1) * n_tok * d * 2 + d * 2 < ((int64_t)1 << 31);
+}
 // Dynamic LDS the generic kernels may request (bytes).
 constexpr int64_t kGenericMaxLds = 64 * 1024;
 // LDS of the generic batched backward: per-(query, row) alpha and da, per-row
@@ -124,9 +153,10 @@ struct BwdBatchedArgs {
 
 // Pure shape arithmetic (sy_plan.cpp). `has_stats` matters to SY_OP_BWD only:
 // whether the forward's logits and r are passed (the operator's path, and what
-// sy_plan_for reports) or recomputed.
+// sy_plan_for reports) or recomputed. `matrix_ok` = 0 leaves the matrix-core
+// batched backward out (its dv offsets do not fit the token count).
 int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_dtype, int aligned,
-              sy_plan* out, int has_stats = 1);
+              sy_plan* out, int has_stats = 1, int matrix_ok = 1);
 
 // Launch-time tile override from the SY_TILE_* environment variables
 // (sy_plan.cpp); sy_plan_for never applies it.
@@ -136,6 +166,12 @@ void apply_tile_override(int op, int64_t n_src, int64_t d, sy_plan* p);
 // matrix_batched_fits). With `info` != nullptr fills it and launches nothing.
 struct KernelRes;
 hipError_t launch_batched_matrix(const BatchedArgs& a, hipStream_t s, KernelRes* info);
+// Launches the matrix-core batched backward on `grid` workgroups (a must pass
+// bwd_matrix_fits and bwd_matrix_offsets_fit; 1 <= grid <= n_tok). With
+// `info` != nullptr fills it (resources and the grid it would choose) and
+// launches nothing.
+hipError_t launch_bwd_batched_matrix(const BwdBatchedArgs& a, int grid, hipStream_t s,
+                                     KernelRes* info);
 
 // Device queries, cached per device (sy_capi.cpp).
 hipError_t cu_count(int* out);

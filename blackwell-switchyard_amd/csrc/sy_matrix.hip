@@ -389,6 +389,382 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
   }
 }
 
+// ------------------------------------------------------------ batched backward
+//
+// Gradient of the batched forward for grad_out g [S][n_tok][D], S <= 8. Per
+// token, with GQ = [g_0 .. g_7 ; q_0 .. q_7] (16 rows, zero past n_q):
+//   D[n][c]  = sum_d V[n][d] GQ[c][d]         v_mfma_f32_16x16x32 (K = d)
+// gives G_sn = <g_s, v_n> (c = s) and the logit dots <q_s, v_n> (c = 8 + s)
+// in one product. Then per (s, n), like the single-query operator,
+//   dlogit = alpha (G - sum_k alpha_k G_k),  da = dlogit r_n,
+//   c_n    = -sum_s dlogit logit r_n^2 / D,
+// and two more products of the token's LDS tile:
+//   dV^T[d][n] = sum_k GQ[k][d] Coef[k][n] + c_n V[n][d]   (Coef = [alpha ; da])
+//   dQ^T[d][s] += sum_n V[n][d] da[s][n]                   (over the tokens)
+// both v_mfma_f32_16x16x16 with the 4x4-transposed LDS read as A operand. The
+// fp32 coefficients are split into high and low 16-bit parts (two MFMAs), so
+// dv keeps fp32-level error before its single rounding and dq accumulates in
+// fp32 registers for the whole kernel (one partial row per query and
+// workgroup, reduced afterwards in a fixed order).
+//
+// Layout of the D[n][c] result: lane (g, i) holds rows n = 4g + j of column
+// i, so lanes i and i ^ 8 hold G and the logit dot of query i & 7 (one DPP
+// row rotation swaps them); the softmax over n runs over j and the four
+// 16-lane groups. That is the B layout of the dq product (k = n, column s);
+// the dv product needs the transpose (k = coefficient, column n), which goes
+// through a 1 KiB LDS table per wave.
+//
+// Work split as in the forward: 4 waves per workgroup, one token at a time,
+// wave w owns D/4 columns, each wave reads back only the LDS rows it wrote;
+// the logit partials cross the waves through LDS once per token. The next
+// token's v and g rows are loaded into registers while the current one is
+// computed. dv rows leave through LDS staging as SC-column row segments, all
+// rows of a store from one buffer resource ((n_src - 1) * stride + D*2 bytes
+// must stay below 2^31, checked by the host). Every global load and store in
+// the loop is unconditional (see k_batched_mx), so the waits are exact.
+//
+// Reference: the batched forward is src/switchyard/triton_op.py:378-501; it
+// has no backward (the single-query derivation is at :205-214).
+template <class T, int KS, int NR>
+__global__ void __launch_bounds__(256, 1)
+k_bwd_batched_mx(const RowTable v, const uint16_t* __restrict__ q, const uint16_t* __restrict__ g,
+                 const RowTable dv, float* __restrict__ partial, int n_src, int n_q,
+                 int64_t n_tok, float eps, float inv_d) {
+  using M = Mx<T>;
+  constexpr int d = 128 * KS;
+  constexpr uint32_t rs = (uint32_t)d * 2u + kMxPad;
+  constexpr uint32_t row_bytes = (uint32_t)d * 2u;
+  constexpr int cpr = 4 * KS;
+  constexpr uint32_t kDrop = 0x80000000u;
+  constexpr int SQ = (int)kBwdMatrixMaxQ;
+  static_assert(SQ == 8, "g and q rows take 8 of the 16 MFMA columns each");
+  // dv staging: SC columns per round, stride SC*2 + 16 bytes; a store covers
+  // kRpi rows with kLpr lanes each.
+  constexpr int SC = NR <= 9 && KS % 8 == 0 ? 256 : 128;
+  static_assert((32 * KS) % SC == 0, "store rounds must tile the wave's columns");
+  constexpr int kRow = SC * 2 + 16;
+  constexpr int kLpr = SC / 8;
+  constexpr int kRpi = 64 / kLpr;
+  constexpr int kRounds = (NR + kRpi - 1) / kRpi;
+  constexpr int kTs = 20;  // coefficient table row stride (floats): [n][k], k = 16 is c_n
+  extern __shared__ __align__(16) char lds[];
+  char* const gq = lds;            // 16 rows: g of the token, then the queries
+  char* const vs = lds + 16 * rs;  // n_src source rows, then a zero row
+  __shared__ __align__(16) float xl[2][kMxWaves][64][4];
+  __shared__ __align__(16) float xs[2][kMxWaves][kMxRows];
+  __shared__ __align__(16) float tt[kMxWaves][16 * kTs];
+  __shared__ __align__(16) char ob[kMxWaves][kRounds * kRpi * kRow];
+
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int qi = lane & 15;
+  const int grp = lane >> 4;
+  const int cb = w * 32 * KS;
+  const uint32_t coff = lane < cpr ? (uint32_t)(cb + 8 * lane) * 2u : kDrop;
+  const int loff = (cb + 8 * lane) * 2;  // this lane's chunk (bytes into a row)
+
+  // Queries (GQ rows 8..15, zero past n_q) and the zero source row.
+  {
+    i32x4_t qv[SQ];
+#pragma unroll
+    for (int s = 0; s < SQ; ++s)
+      qv[s] = ld16(make_rsrc(q + (int64_t)(s < n_q ? s : 0) * d, s < n_q ? row_bytes : 0u), coff);
+    if (lane < cpr) {
+#pragma unroll
+      for (int s = 0; s < SQ; ++s) *(i32x4_t*)(gq + (8 + s) * rs + loff) = qv[s];
+      *(i32x4_t*)(vs + n_src * rs + loff) = i32x4_t{0, 0, 0, 0};
+    }
+  }
+
+  f32x4_t qacc[KS / 2][4];
+#pragma unroll
+  for (int b = 0; b < KS / 2; ++b)
+#pragma unroll
+    for (int a = 0; a < 4; ++a) qacc[b][a] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const int64_t step = gridDim.x;
+  const int64_t first = blockIdx.x;
+  const int iters = first < n_tok ? (int)((n_tok - first + step - 1) / step) : 0;
+
+  auto stage = [&](i32x4_t (&sv)[NR], i32x4_t (&sg)[SQ], int64_t t) {
+    const bool tok_ok = t < n_tok;
+    const int64_t tc = tok_ok ? t : n_tok - 1;
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      const bool real = n < n_src && tok_ok;
+      sv[n] = ld16_stream(make_rsrc(row_at<false, const uint16_t>(v, n < n_src ? n : 0) + tc * d,
+                                    real ? row_bytes : 0u),
+                          coff);
+    }
+#pragma unroll
+    for (int s = 0; s < SQ; ++s) {
+      const bool real = s < n_q && tok_ok;
+      sg[s] = ld16_stream(
+          make_rsrc(g + ((int64_t)(s < n_q ? s : 0) * n_tok + tc) * d, real ? row_bytes : 0u),
+          coff);
+    }
+  };
+  auto commit = [&](const i32x4_t (&sv)[NR], const i32x4_t (&sg)[SQ]) {
+    wave_lds_fence();
+    if (lane < cpr) {
+#pragma unroll
+      for (int n = 0; n < NR; ++n)
+        if (n < n_src) *(i32x4_t*)(vs + n * rs + loff) = sv[n];
+#pragma unroll
+      for (int s = 0; s < SQ; ++s) *(i32x4_t*)(gq + s * rs + loff) = sg[s];
+    }
+    wave_lds_fence();
+  };
+
+  // Logits A operand: source row qi (zero row past n_src); B: GQ row qi.
+  const int ra = qi < n_src ? qi : n_src;
+  const char* const abase = vs + ra * rs + (cb + 8 * grp) * 2;
+  const char* const bbase = gq + qi * rs + (cb + 8 * grp) * 2;
+  // Transposed reads (A of both output products): row 4*grp + qi/4 of GQ and
+  // of V, at the forward's bank-conflict-free column pieces.
+  const uint32_t toff = (uint32_t)cb * 2u + 8u * (qi & 1) + 64u * ((qi >> 1) & 1);
+  const int kt = 4 * grp + (qi >> 2);
+  const char* const tgq = gq + kt * rs + toff;
+  const char* const tvs = vs + (kt < n_src ? kt : n_src) * rs + toff;
+  auto tread = [&](const char* base, int b, int a) {
+    return __builtin_bit_cast(i32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                           (lds_s16x4_t*)(base + b * 128 + a * 16)));
+  };
+  // Output layout of MFMA a of a 64-column block: lane (grp, qi) holds row n = qi
+  // (dv) or query s = qi (dq) at local columns 8a + ocol + j, j < 4.
+  const int ocol = 4 * (grp & 1) + 32 * (grp >> 1);
+  const char* const cvb = vs + ra * rs + (cb + ocol) * 2;
+  float* const tw = tt[w];
+  char* const obw = ob[w];
+  const uint32_t dv_stride = (uint32_t)dv.stride_bytes;
+  const uint32_t dv_bytes = (uint32_t)(n_src - 1) * dv_stride + row_bytes;
+  const bool gl = qi < 8;  // column qi is G (else the logit dot of query qi - 8)
+
+  auto token = [&](int k, int64_t tok) {
+    // 1. D[n][c] partials over this wave's columns, and the sums of squares.
+    constexpr int kAhead = 4;
+    f32x4_t acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+    float ss0 = 0.0f, ss1 = 0.0f;
+    i32x4_t wa[kAhead], wb[kAhead];
+#pragma unroll
+    for (int kk = 0; kk < kAhead && kk < KS; ++kk) {
+      wa[kk] = *(const i32x4_t*)(abase + kk * 64);
+      wb[kk] = *(const i32x4_t*)(bbase + kk * 64);
+    }
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      const i32x4_t a = wa[kk % kAhead], b = wb[kk % kAhead];
+      if (kk + kAhead < KS) {
+        wa[kk % kAhead] = *(const i32x4_t*)(abase + (kk + kAhead) * 64);
+        wb[kk % kAhead] = *(const i32x4_t*)(bbase + (kk + kAhead) * 64);
+      }
+      if (kk % 2 == 0) {
+        ss0 = dot<T>(a, a, ss0);
+        acc0 = M::k32(a, b, acc0);
+      } else {
+        ss1 = dot<T>(a, a, ss1);
+        acc1 = M::k32(a, b, acc1);
+      }
+      // Keep the read window: at one wave per SIMD the scheduler would
+      // otherwise hoist every read of the token.
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const f32x4_t acc = acc0 + acc1;
+    float ss = ss0 + ss1;
+    ss += __shfl_xor(ss, 16);
+    ss += __shfl_xor(ss, 32);
+    const int xb = k & 1;
+    *(f32x4_t*)&xl[xb][w][lane][0] = acc;
+    if (lane < kMxRows) xs[xb][w][lane] = ss;
+    __syncthreads();
+    f32x4_t lt = *(const f32x4_t*)&xl[xb][0][lane][0];
+    f32x4_t sq = *(const f32x4_t*)&xs[xb][0][4 * grp];
+#pragma unroll
+    for (int ww = 1; ww < kMxWaves; ++ww) {
+      lt += *(const f32x4_t*)&xl[xb][ww][lane][0];
+      sq += *(const f32x4_t*)&xs[xb][ww][4 * grp];
+    }
+
+    // 2. Softmax of query qi & 7 over rows n = 4*grp + j (j, then the groups).
+    float G[4], lgr[4], lg[4], r[4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float o = dpp<0x128>(lt[j]);  // row_ror:8: the lane qi ^ 8 value
+      G[j] = gl ? lt[j] : o;
+      r[j] = rsqrtf(fmaf(sq[j], inv_d, eps));
+      lgr[j] = (gl ? o : lt[j]) * r[j];
+      lg[j] = 4 * grp + j < n_src ? lgr[j] : -INFINITY;
+      mx = fmaxf(mx, lg[j]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    float p[4];
+    int top = 64;  // first row at the maximum
+#pragma unroll
+    for (int j = 3; j >= 0; --j) {
+      const bool real = 4 * grp + j < n_src;
+      p[j] = real ? expf(lg[j] - mx) : 0.0f;
+      if (real && lg[j] == mx) top = 4 * grp + j;
+    }
+    float ls = (p[0] + p[1]) + (p[2] + p[3]);
+    ls += __shfl_xor(ls, 16);
+    ls += __shfl_xor(ls, 32);
+    top = min(top, __shfl_xor(top, 16));
+    top = min(top, __shfl_xor(top, 32));
+    // G of the top row (lane (top / 4, qi), element top % 4): the dots are
+    // taken relative to it, as in the single-query backward.
+    const int tj = top & 3;
+    const float gsel = tj == 0 ? G[0] : tj == 1 ? G[1] : tj == 2 ? G[2] : G[3];
+    const float gref = __shfl(gsel, ((top >> 2) & 3) * 16 + qi);
+    const float inv_l = 1.0f / ls;
+    float al[4], dg[4];
+    float sdev = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      al[j] = p[j] * inv_l;
+      dg[j] = G[j] - gref;
+      sdev = fmaf(al[j], dg[j], sdev);
+    }
+    sdev += __shfl_xor(sdev, 16);
+    sdev += __shfl_xor(sdev, 32);
+    float da[4], cn4[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float dl = al[j] * (dg[j] - sdev);
+      da[j] = dl * r[j];
+      // c_n: sum over the 8 queries, lanes qi & 7 (both halves of a row agree)
+      float c = -dl * lgr[j] * (r[j] * r[j] * inv_d);
+      c += dpp<0xB1>(c);   // quad_perm [1,0,3,2]
+      c += dpp<0x4E>(c);   // quad_perm [2,3,0,1]
+      c += dpp<0x141>(c);  // row_half_mirror
+      cn4[j] = c;
+    }
+
+    // 3. Coefficients of the dv product, transposed through LDS:
+    //    tw[n][k] = alpha[k][n] (k < 8), da[k - 8][n] (k >= 8); tw[n][16] = c_n.
+    wave_lds_fence();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) tw[(4 * grp + j) * kTs + qi] = gl ? al[j] : da[j];
+    if (qi == 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) tw[(4 * grp + j) * kTs + 16] = cn4[j];
+    }
+    wave_lds_fence();
+    const f32x4_t cf = *(const f32x4_t*)&tw[qi * kTs + 4 * grp];
+    const float cn = tw[qi * kTs + 16];
+    const int c01 = M::pack2(cf[0], cf[1]), c23 = M::pack2(cf[2], cf[3]);
+    const i32x2_t ch = {c01, c23};
+    const i32x2_t cl = {M::pack2(cf[0] - M::lo(c01), cf[1] - M::hi(c01)),
+                        M::pack2(cf[2] - M::lo(c23), cf[3] - M::hi(c23))};
+    // B of the dq product: da[s = qi][n = 4*grp + j], columns 8..15 zero.
+    float db[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) db[j] = gl ? da[j] : 0.0f;
+    const int d01 = M::pack2(db[0], db[1]), d23 = M::pack2(db[2], db[3]);
+    const i32x2_t dh = {d01, d23};
+    const i32x2_t dlo = {M::pack2(db[0] - M::lo(d01), db[1] - M::hi(d01)),
+                         M::pack2(db[2] - M::lo(d23), db[3] - M::hi(d23))};
+
+    // 4. dv (staged, SC columns per store round) and dq, 64 columns a block.
+    constexpr int kBlocks = KS / 2;
+    constexpr int kPerStage = SC / 64;
+    const auto dr = make_rsrc(row_at<false, uint16_t>(dv, 0) + tok * d, dv_bytes);
+    // Operands of a block (A of both products, v for c_n v), read one block
+    // ahead of their MFMAs; scheduling barriers keep that window.
+    i32x2_t ag[2][4], av[2][4], vv[2][4];
+    auto operands = [&](int b, int u) {
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        ag[u][a] = tread(tgq, b, a);
+        av[u][a] = tread(tvs, b, a);
+        vv[u][a] = *(const i32x2_t*)(cvb + (b * 64 + 8 * a) * 2);
+      }
+    };
+    operands(0, 0);
+#pragma unroll
+    for (int b = 0; b < kBlocks; ++b) {
+      const int u = b & 1;
+      if (b % kPerStage == 0) wave_lds_fence();
+      if (b + 1 < kBlocks) operands(b + 1, u ^ 1);
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        f32x4_t c = {0.0f, 0.0f, 0.0f, 0.0f};
+        c = M::k16(ag[u][a], cl, c);
+        c = M::k16(ag[u][a], ch, c);
+        qacc[b][a] = M::k16(av[u][a], dlo, qacc[b][a]);
+        qacc[b][a] = M::k16(av[u][a], dh, qacc[b][a]);
+        const i32x2_t x = vv[u][a];
+        const float f0 = fmaf(cn, M::lo(x[0]), c[0]);
+        const float f1 = fmaf(cn, M::hi(x[0]), c[1]);
+        const float f2 = fmaf(cn, M::lo(x[1]), c[2]);
+        const float f3 = fmaf(cn, M::hi(x[1]), c[3]);
+        const i32x2_t o = {M::pack2(f0, f1), M::pack2(f2, f3)};
+        if (qi < n_src) *(i32x2_t*)(obw + qi * kRow + ((b % kPerStage) * 64 + 8 * a + ocol) * 2) = o;
+      }
+      if (b % kPerStage == kPerStage - 1) {
+        wave_lds_fence();
+        const int col0 = cb + 64 * (b + 1 - kPerStage);
+        const int chunk = lane % kLpr;
+        i32x4_t vals[kRounds];
+#pragma unroll
+        for (int rr = 0; rr < kRounds; ++rr)
+          vals[rr] = *(const i32x4_t*)(obw + (kRpi * rr + lane / kLpr) * kRow + chunk * 16);
+#pragma unroll
+        for (int rr = 0; rr < kRounds; ++rr) {
+          const int row = kRpi * rr + lane / kLpr;
+          st16_stream(dr,
+                      row < n_src ? (uint32_t)row * dv_stride + (uint32_t)(col0 + 8 * chunk) * 2u
+                                  : kDrop,
+                      vals[rr]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  if (iters > 0) {
+    // Stores one token issues.
+    constexpr int kTokenStores = (32 * KS / SC) * kRounds;
+    i32x4_t sva[NR], sga[SQ], svb[NR], sgb[SQ];
+    stage(sva, sga, first);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): queries and the first token
+    commit(sva, sga);
+    stage(svb, sgb, first + step);
+    // Dropped stores, so that the loads of the second set are followed by as
+    // many memory operations as on every later pass (exact waits).
+    __builtin_amdgcn_sched_barrier(0);
+    {
+      const auto none = make_rsrc(partial, 0u);
+#pragma unroll
+      for (int i = 0; i < kTokenStores; ++i) st16_stream(none, 16u * i, i32x4_t{0, 0, 0, 0});
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // Pairs of tokens, then the odd one (a break inside the pair would make
+    // the compiler copy the dq accumulators between register files).
+    int k = 0;
+    for (; k + 1 < iters; k += 2) {
+      const int64_t tok = first + (int64_t)k * step;
+      stage(sva, sga, tok + 2 * step);
+      token(k, tok);
+      commit(svb, sgb);
+      stage(svb, sgb, tok + 3 * step);
+      token(k + 1, tok + step);
+      if (k + 2 < iters) commit(sva, sga);
+    }
+    if (k < iters) token(k, first + (int64_t)k * step);
+  }
+
+  // dq partial row of each query: partial[blockIdx][s][:].
+  if (qi < n_q) {
+    float* const pr = partial + ((int64_t)blockIdx.x * n_q + qi) * d + cb + ocol;
+#pragma unroll
+    for (int b = 0; b < KS / 2; ++b)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) *(f32x4_t*)(pr + b * 64 + 8 * a) = qacc[b][a];
+  }
+}
+
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 template <class T, int KS, int NR, int SQ>
@@ -443,7 +819,68 @@ hipError_t launch_mx_dtype(const BatchedArgs& a, hipStream_t s, KernelRes* info)
   }
 }
 
+template <class T, int KS, int NR>
+hipError_t launch_bmx(const BwdBatchedArgs& a, int grid, hipStream_t s, KernelRes* info) {
+  const size_t lds = (size_t)bwd_matrix_dynamic_lds(a.n_src, a.d);
+  auto* kern = k_bwd_batched_mx<T, KS, NR>;
+  KernelRes r{0, 0, 1, 0};
+  static hipFuncAttributes fa;
+  static const hipError_t fa_err =
+      hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(kern));
+  hipError_t e = fa_err;
+  if (e != hipSuccess) return e;
+  r.vgprs = fa.numRegs;
+  r.lds = (int)(fa.sharedSizeBytes + lds);
+  const int alloc = std::max(8, ((fa.numRegs + 7) / 8) * 8);
+  const int by_waves = std::min(8, 512 / alloc);  // one wave per SIMD per workgroup
+  r.blocks_per_cu = std::max(1, std::min(by_waves, (160 * 1024) / std::max(1, r.lds)));
+  int cus = 0;
+  if (cu_count(&cus) != hipSuccess || cus < 1) cus = 1;
+  r.grid = (int)std::max<int64_t>(1, std::min<int64_t>((int64_t)cus * r.blocks_per_cu, a.n_tok));
+  if (info != nullptr) {
+    *info = r;
+    return hipSuccess;
+  }
+  // Every workgroup needs a token: the dq partial rows are the grid's.
+  if (grid < 1 || grid > a.n_tok) return hipErrorInvalidConfiguration;
+  if (lds > 64 * 1024) {
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kMxWaves), lds, s, a.v, (const uint16_t*)a.q,
+                     (const uint16_t*)a.g, a.dv, a.partial, a.n_src, a.n_q, a.n_tok, a.eps,
+                     1.0f / (float)a.d);
+  return hipGetLastError();
+}
+
+template <class T, int KS>
+hipError_t launch_bmx_rows(const BwdBatchedArgs& a, int grid, hipStream_t s, KernelRes* info) {
+  return a.n_src <= 9 ? launch_bmx<T, KS, 9>(a, grid, s, info)
+                      : launch_bmx<T, KS, 16>(a, grid, s, info);
+}
+
+template <class T>
+hipError_t launch_bmx_dtype(const BwdBatchedArgs& a, int grid, hipStream_t s, KernelRes* info) {
+  switch (a.d / 128) {
+    case 4: return launch_bmx_rows<T, 4>(a, grid, s, info);
+    case 8: return launch_bmx_rows<T, 8>(a, grid, s, info);
+    case 12: return launch_bmx_rows<T, 12>(a, grid, s, info);
+    case 16: return launch_bmx_rows<T, 16>(a, grid, s, info);
+    default: return hipErrorInvalidConfiguration;
+  }
+}
+
 }  // namespace
+
+hipError_t launch_bwd_batched_matrix(const BwdBatchedArgs& a, int grid, hipStream_t s,
+                                     KernelRes* info) {
+  if (!bwd_matrix_fits(a.n_src, a.n_q, a.d, a.dtype)) return hipErrorInvalidConfiguration;
+  if (!bwd_matrix_offsets_fit(a.n_src, a.n_tok, a.d)) return hipErrorInvalidConfiguration;
+  if (a.n_tok == 0) return hipSuccess;
+  return a.dtype == SY_BF16 ? launch_bmx_dtype<BF16>(a, grid, s, info)
+                            : launch_bmx_dtype<F16>(a, grid, s, info);
+}
 
 hipError_t launch_batched_matrix(const BatchedArgs& a, hipStream_t s, KernelRes* info) {
   if (!matrix_batched_fits(a.n_src, a.n_q, a.d, a.dtype)) return hipErrorInvalidConfiguration;

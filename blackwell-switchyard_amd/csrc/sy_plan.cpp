@@ -26,9 +26,12 @@
 //     1536, 2048} run on the matrix cores (config 3: 8 queries x 9 rows is ~7000
 //     VALU instructions a token on the register tile); otherwise resident with
 //     S <= 16, else one forward launch per query.
-//  6. Batched backward: one chunk per lane on the fewest waves that cover the
-//     row, N <= 9 and S <= 8 (dv and dq accumulators stay in registers);
-//     otherwise the generic kernel while its LDS scalars fit.
+//  6. Batched backward: 16-bit inputs with S <= 8, D in {512, 1024, 1536,
+//     2048}, N <= 16 (N <= 9 at D = 2048) and the workgroup's LDS within
+//     160 KiB run on the matrix cores, unless the caller says its dv offsets
+//     do not fit; otherwise one chunk per lane on the fewest waves that cover the row,
+//     N <= 9 and S <= 8 (dv and dq accumulators stay in registers); otherwise
+//     the generic kernel while its LDS scalars fit.
 #include <cstdio>
 #include <cstdlib>
 
@@ -102,7 +105,7 @@ bool resident(int64_t n_src, int64_t e, int budget, int max_vpl, int* w_out, int
 }  // namespace
 
 int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_dtype,
-              int aligned, sy_plan* out, int has_stats) {
+              int aligned, sy_plan* out, int has_stats, int matrix_ok) {
   if (out == nullptr) return SY_ERR_NULL;
   if (op < SY_OP_FWD || op > SY_OP_BWD_BATCHED) return SY_ERR_OP;
   if (!valid_dtype(v_dtype) || !valid_dtype(w_dtype)) return SY_ERR_DTYPE;
@@ -117,6 +120,17 @@ int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_
   int w = 0, vpl = 0, nr = 0;
 
   if (op == SY_OP_BWD_BATCHED) {
+    if (vec && matrix_ok && bwd_matrix_fits(n_src, n_q, d, v_dtype)) {
+      out->family = SY_FAMILY_MATRIX;
+      out->waves_per_token = 4;
+      out->chunks_per_lane = 1;
+      out->rows_per_tile = n_src <= 9 ? 9 : 16;
+      out->elems_per_chunk = ce;
+      out->block_threads = 256;
+      out->tokens_per_block = 1;
+      out->n_chunks = 1;
+      return SY_OK;
+    }
     if (vec && n_src <= kBwdBatchedMaxN && n_q <= kBwdBatchedMaxQ) {
       for (int ww : kWaves) {
         if ((int64_t)64 * ww < e) continue;

@@ -282,12 +282,18 @@ def test_backward_takes_four_chunks_only_with_one_wave_per_simd():
 
 
 def test_batched_backward_plan():
-    # one chunk per lane on the fewest waves that cover the row; N <= 9, S <= 8
-    p = plan(_lib.OP_BWD_BATCHED, 9, 2048, n_q=8)
+    # matrix cores: 16-bit, S <= 8, D in {512, 1024, 1536, 2048}, N <= 16 (N <= 9 at 2048)
+    for dt in (torch.bfloat16, torch.float16):
+        for n, s, d in ((9, 8, 2048), (1, 1, 512), (16, 8, 1536), (12, 3, 1024), (4, 3, 512)):
+            p = plan(_lib.OP_BWD_BATCHED, n, d, dt, n_q=s)
+            assert (p["family_name"], p["waves_per_token"], p["rows_per_tile"]) == \
+                ("matrix", 4, 9 if n <= 9 else 16), (n, s, d, dt)
+    # else one chunk per lane on the fewest waves that cover the row; N <= 9, S <= 8
+    p = plan(_lib.OP_BWD_BATCHED, 9, 2048, torch.float32, n_q=8)
     assert (p["family_name"], p["waves_per_token"], p["chunks_per_lane"], p["rows_per_tile"]) == \
-        ("resident", 4, 1, 9)
+        ("resident", 8, 1, 9)
     assert plan(_lib.OP_BWD_BATCHED, 4, 4096, n_q=3)["waves_per_token"] == 8
-    assert plan(_lib.OP_BWD_BATCHED, 4, 512, n_q=3)["rows_per_tile"] == 4
+    assert plan(_lib.OP_BWD_BATCHED, 4, 1024, torch.float32, n_q=3)["rows_per_tile"] == 4
     assert plan(_lib.OP_BWD_BATCHED, 9, 2048, torch.float32, n_q=2)["waves_per_token"] == 8
     for n, s, d in ((10, 8, 2048), (9, 9, 2048), (9, 8, 8192), (5, 3, 777)):
         assert plan(_lib.OP_BWD_BATCHED, n, d, n_q=s)["family_name"] == "generic", (n, s, d)

@@ -272,6 +272,31 @@ def test_batched_backward(nstd, dtype):
     _close(qq.grad.cpu(), rdq, dtype, what="dq")
 
 
+@pytest.mark.parametrize("nstd", [(9, 8, 1100, 2048), (9, 2, 257, 2048), (16, 5, 517, 1536),
+                                  (1, 8, 300, 512), (13, 7, 777, 1024), (6, 1, 100, 2048)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_batched_backward_matrix_kernel(nstd, dtype):
+    """The matrix-core batched backward (16-bit inputs, S <= 8): dv and dq
+    against the C oracle, over token counts that give the workgroups an odd
+    and an even number of tokens, fewer tokens than CUs, a single source (dq
+    is then exactly zero) and a single query."""
+    n, s, t, d = nstd
+    assert _lib.plan(_lib.OP_BWD_BATCHED, n, d, dtype, n_q=s)["family_name"] == "matrix"
+    print(f"matrix batched bwd {nstd} {dtype}", flush=True)
+    v, _ = _make(n, t, d, dtype, seed=31)
+    gen = torch.Generator().manual_seed(32)
+    q = (torch.randn(s, d, generator=gen) * 2.0 / d**0.5).to(dtype).to(DEV)
+    g = torch.randn(s, 1, t, d, generator=gen).to(dtype).to(DEV)
+    vv, qq = v.clone().requires_grad_(), q.clone().requires_grad_()
+    block_attn_res_batched_train(vv, qq).backward(g)
+    rdv, rdq = c_oracle.batched_backward(_np(v)[:, 0], _np(q), _np(g)[:, 0])
+    _close(vv.grad[:, 0].cpu(), rdv, dtype, what="dv")
+    if n == 1:
+        assert not qq.grad.any()
+    else:
+        _close(qq.grad.cpu(), rdq, dtype, what="dq")
+
+
 def test_batched_backward_is_deterministic_and_single_query_consistent():
     v, w = _make(9, 128, 2048, torch.bfloat16, seed=13)
     g = torch.randn(1, 1, 128, 2048, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).to(DEV)
