@@ -66,9 +66,10 @@ int bwd_grid(const sy_plan& p, int64_t n_tok, int dtype, bool stats, int variant
 // Plan of the batched backward for this token count: the matrix-core kernel
 // only where its dv offsets fit.
 int bwd_batched_plan(int64_t n_src, int64_t n_q, int64_t n_tok, int64_t d, int dtype, int aligned,
-                     sy_plan* p) {
+                     int64_t v_stride_bytes, sy_plan* p) {
   int rc = make_plan(SY_OP_BWD_BATCHED, n_src, n_q, d, dtype, dtype, aligned, p);
-  if (rc == SY_OK && p->family == SY_FAMILY_MATRIX && !bwd_matrix_offsets_fit(n_src, n_tok, d))
+  if (rc == SY_OK && p->family == SY_FAMILY_MATRIX &&
+      !bwd_matrix_offsets_fit(n_src, n_tok, d, v_stride_bytes))
     rc = make_plan(SY_OP_BWD_BATCHED, n_src, n_q, d, dtype, dtype, aligned, p, 1, 0);
   return rc;
 }
@@ -576,14 +577,18 @@ int64_t sy_bwd_batched_workspace_bytes(int64_t n_src, int64_t n_q, int64_t n_tok
   if (n_q < 1 || n_q > 0x7fffffff) return SY_ERR_SHAPE;
   if (n_tok == 0) return 0;
   int64_t g = 0;
+  // Every plan sy_bwd_batched may pick (it depends on alignment and, for the
+  // matrix kernel, on the source stride).
   for (int aligned : {1, 0}) {
-    sy_plan p;
-    rc = bwd_batched_plan(n_src, n_q, n_tok, d, dtype, aligned, &p);
-    if (rc != SY_OK) return rc;
-    int gi = 0;
-    rc = bwd_batched_grid(p, n_src, n_q, n_tok, d, dtype, &gi);
-    if (rc != SY_OK) return rc;
-    if (gi > g) g = gi;
+    for (int matrix_ok : {1, 0}) {
+      sy_plan p;
+      rc = make_plan(SY_OP_BWD_BATCHED, n_src, n_q, d, dtype, dtype, aligned, &p, 1, matrix_ok);
+      if (rc != SY_OK) return rc;
+      int gi = 0;
+      rc = bwd_batched_grid(p, n_src, n_q, n_tok, d, dtype, &gi);
+      if (rc != SY_OK) return rc;
+      if (gi > g) g = gi;
+    }
   }
   return g * n_q * d * (int64_t)sizeof(float);
 }
@@ -606,7 +611,7 @@ int sy_bwd_batched(const void* v, const void* queries, const void* grad_out, voi
   const bool aligned = vec_rows(vok && dok, d, dtype) && al16(queries) && al16(grad_out) &&
                        al16(workspace);
   sy_plan p;
-  rc = bwd_batched_plan(n_src, n_q, n_tok, d, dtype, aligned, &p);
+  rc = bwd_batched_plan(n_src, n_q, n_tok, d, dtype, aligned, src_stride * esize(dtype), &p);
   if (rc != SY_OK) return rc;
   int grid = 0;
   if (n_tok != 0) {

@@ -334,7 +334,8 @@ k_bwd_batched_generic(const RowTable v, const void* __restrict__ q, const void* 
   }
 }
 
-// dw[c] = sum over rows r of partial[r][c], in a fixed order: wave q of the
+// dw[c] = sum over rows r of partial[r][c] (scalar path: any D, any
+// alignment), in a fixed order: wave q of the
 // 1024-thread workgroup sums rows [q*rows/16, (q+1)*rows/16) in sequence, then
 // the 16 wave sums are added in wave order. Same inputs, same bits.
 __global__ void __launch_bounds__(1024)
@@ -355,6 +356,57 @@ k_dw_reduce(const float* __restrict__ partial, int rows, int d, void* __restrict
 #pragma unroll
     for (int q = 1; q < 16; ++q) t += sh[q][lane];
     store_elem(dw, col, t, wt);
+  }
+}
+
+// dw[c] = sum over rows of partial[r][c], 16-byte path (D % 4 == 0, rows
+// 16-byte aligned). A workgroup owns 64 columns: lane l of wave w is column
+// group l % 16 (four columns) and row lane rl = 4w + l / 16, which sums rows
+// rl, rl + 64, rl + 128, ... in that order (four loads in flight per step);
+// the 64 row-lane sums are then added pairwise in a fixed tree (row lane i
+// takes i + 32, then i + 16, ...). Same inputs, same bits.
+__global__ void __launch_bounds__(1024)
+k_dw_reduce4(const float* __restrict__ partial, int rows, int d, void* __restrict__ dw, int wt) {
+  __shared__ float4 sh[64][16];
+  const int lane = threadIdx.x & 63;
+  const int cl = lane & 15;
+  const int rl = (threadIdx.x >> 6) * 4 + (lane >> 4);
+  const int n4 = d / 4;
+  const int c4 = blockIdx.x * 16 + cl;
+  const float4* __restrict__ p4 = reinterpret_cast<const float4*>(partial);
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (c4 < n4) {
+    int r = rl;
+    for (; r + 3 * 64 < rows; r += 4 * 64) {
+      const float4 a = p4[(int64_t)r * n4 + c4];
+      const float4 b = p4[(int64_t)(r + 64) * n4 + c4];
+      const float4 c = p4[(int64_t)(r + 128) * n4 + c4];
+      const float4 e = p4[(int64_t)(r + 192) * n4 + c4];
+      acc.x += a.x; acc.y += a.y; acc.z += a.z; acc.w += a.w;
+      acc.x += b.x; acc.y += b.y; acc.z += b.z; acc.w += b.w;
+      acc.x += c.x; acc.y += c.y; acc.z += c.z; acc.w += c.w;
+      acc.x += e.x; acc.y += e.y; acc.z += e.z; acc.w += e.w;
+    }
+    for (; r < rows; r += 64) {
+      const float4 a = p4[(int64_t)r * n4 + c4];
+      acc.x += a.x; acc.y += a.y; acc.z += a.z; acc.w += a.w;
+    }
+  }
+  sh[rl][cl] = acc;
+#pragma unroll
+  for (int h = 32; h >= 1; h /= 2) {
+    __syncthreads();
+    if (rl < h) {
+      const float4 o = sh[rl + h][cl];
+      acc.x += o.x; acc.y += o.y; acc.z += o.z; acc.w += o.w;
+      sh[rl][cl] = acc;
+    }
+  }
+  if (rl == 0 && c4 < n4) {
+    store_elem(dw, 4 * (int64_t)c4, acc.x, wt);
+    store_elem(dw, 4 * (int64_t)c4 + 1, acc.y, wt);
+    store_elem(dw, 4 * (int64_t)c4 + 2, acc.z, wt);
+    store_elem(dw, 4 * (int64_t)c4 + 3, acc.w, wt);
   }
 }
 
@@ -440,8 +492,13 @@ hipError_t launch_bwd_batched_generic(const BwdBatchedArgs& a, int grid, hipStre
 
 hipError_t launch_dw_reduce(const float* partial, int rows, int d, void* dw, int w_dtype,
                             hipStream_t s) {
-  hipLaunchKernelGGL(k_dw_reduce, dim3((unsigned)((d + 63) / 64)), dim3(1024), 0, s, partial, rows,
-                     d, dw, w_dtype);
+  if (d % 4 == 0 && ((uintptr_t)partial & 15) == 0) {
+    hipLaunchKernelGGL(k_dw_reduce4, dim3((unsigned)((d / 4 + 15) / 16)), dim3(1024), 0, s, partial,
+                       rows, d, dw, w_dtype);
+  } else {
+    hipLaunchKernelGGL(k_dw_reduce, dim3((unsigned)((d + 63) / 64)), dim3(1024), 0, s, partial,
+                       rows, d, dw, w_dtype);
+  }
   return hipGetLastError();
 }
 

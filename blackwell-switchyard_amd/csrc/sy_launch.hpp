@@ -53,20 +53,31 @@ inline bool matrix_batched_offsets_fit(int64_t n_q, int64_t n_tok, int64_t d) {
 // {512, 1024, 1536, 2048}, and the workgroup's LDS within 160 KiB: 16 rows of
 // g and queries, the source rows and a zero row (dynamic), plus the logit
 // exchange, the coefficient tables and the dv staging (static, the kernel's
-// own arithmetic: 9 or 16 staged rows, 256- or 128-column store rounds).
-// The 16-row tile at D = 2048 would spill registers: there N <= 9.
-// Its dv stores address all source rows of a token from one buffer resource:
-// (n_src - 1) * n_tok * D * 2 + D * 2 bytes must stay below 2^31.
+// own arithmetic: 9 or 16 staged rows, SC-column store rounds). Eight waves
+// per workgroup (two per SIMD) at D = 1024 and 2048 (config 3 on MI355X:
+// 103.6 vs 105.9 us with four; D = 1024: 66.6 vs 67.8 us), four at D = 512
+// (N=4 S=8: 41.5 vs 48.6 us) and 1536. The 16-row tile at D = 2048 would
+// spill registers: there N <= 9. Buffer offsets stay below 2^31: the dv rows
+// of a token (n_src - 1 strides) and the rows one staging load covers.
 constexpr int64_t kBwdMatrixMaxQ = 8;
+constexpr int bwd_matrix_waves(int64_t d) { return d == 1024 || d == 2048 ? 8 : 4; }
+// dv store round width (columns) of the (rows, 32-column steps, waves) tile.
+constexpr int bwd_matrix_store_cols(int nr, int ks, int w) {
+  return w == 8 ? (ks >= 8 ? 64 : (32 * ks < 128 ? 32 * ks : 128))
+                : (nr <= 9 && ks % 8 == 0 ? 256 : 128);
+}
 inline int64_t bwd_matrix_dynamic_lds(int64_t n_src, int64_t d) {
   return (16 + n_src + 1) * (d * 2 + 16);
 }
 inline int64_t bwd_matrix_lds(int64_t n_src, int64_t d) {
+  const int w = bwd_matrix_waves(d);
+  const int ks = (int)(d / (32 * w));
   const int64_t nr = n_src <= 9 ? 9 : 16;
-  const int64_t sc = nr <= 9 && (d / 128) % 8 == 0 ? 256 : 128;
+  const int64_t sc = bwd_matrix_store_cols((int)nr, ks, w);
   const int64_t rows_per_store = 64 / (sc / 8);
-  const int64_t staged = (nr + rows_per_store - 1) / rows_per_store * rows_per_store;
-  const int64_t fixed = 2 * 4 * 64 * 16 + 2 * 4 * 16 * 4 + 4 * 16 * 20 * 4 + 4 * staged * (sc * 2 + 16);
+  const int64_t rounds = (nr + rows_per_store - 1) / rows_per_store * rows_per_store;
+  const int64_t staged = rounds > nr ? rounds : nr + 1;
+  const int64_t fixed = w * (2 * 64 * 16 + 2 * 16 * 4 + 24 * 20 * 4 + staged * (sc * 2 + 16));
   return fixed + bwd_matrix_dynamic_lds(n_src, d);
 }
 inline bool bwd_matrix_fits(int64_t n_src, int64_t n_q, int64_t d, int dtype) {
@@ -74,8 +85,13 @@ inline bool bwd_matrix_fits(int64_t n_src, int64_t n_q, int64_t d, int dtype) {
          n_q >= 1 && n_q <= kBwdMatrixMaxQ && (d == 512 || d == 1024 || d == 1536 || d == 2048) &&
          (n_src <= 9 || d < 2048) && bwd_matrix_lds(n_src, d) <= 160 * 1024;
 }
-inline bool bwd_matrix_offsets_fit(int64_t n_src, int64_t n_tok, int64_t d) {
-  return (n_src - 1) * n_tok * d * 2 + d * 2 < ((int64_t)1 << 31);
+inline bool bwd_matrix_offsets_fit(int64_t n_src, int64_t n_tok, int64_t d, int64_t v_stride_bytes) {
+  const int64_t cpr = d / (8 * bwd_matrix_waves(d));  // 16-byte chunks of a wave's slice
+  const int64_t rpl = cpr <= 32 && 64 % cpr == 0 ? 64 / cpr : 1;  // rows per staging load
+  const int64_t g_stride = n_tok * d * 2;  // g and dv rows
+  const int64_t limit = ((int64_t)1 << 31) - d * 2;
+  return (n_src - 1) * g_stride < limit && (rpl - 1) * g_stride < limit &&
+         (rpl - 1) * v_stride_bytes < limit;
 }
 // Dynamic LDS the generic kernels may request (bytes).
 constexpr int64_t kGenericMaxLds = 64 * 1024;

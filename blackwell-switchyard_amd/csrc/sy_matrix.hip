@@ -29,6 +29,7 @@
 // Reference: the batched forward of src/switchyard/triton_op.py:378-501 (same
 // math as S calls of the single-query operator, one read of v).
 #include <algorithm>
+#include <cstdlib>
 
 #include "sy_launch.hpp"
 
@@ -398,11 +399,13 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
 // in one product. Then per (s, n), like the single-query operator,
 //   dlogit = alpha (G - sum_k alpha_k G_k),  da = dlogit r_n,
 //   c_n    = -sum_s dlogit logit r_n^2 / D,
-// and two more products of the token's LDS tile:
-//   dV^T[d][n] = sum_k GQ[k][d] Coef[k][n] + c_n V[n][d]   (Coef = [alpha ; da])
-//   dQ^T[d][s] += sum_n V[n][d] da[s][n]                   (over the tokens)
-// both v_mfma_f32_16x16x16 with the 4x4-transposed LDS read as A operand. The
-// fp32 coefficients are split into high and low 16-bit parts (two MFMAs), so
+// and two more products of the token's LDS tile with one A operand,
+// A[d][k] = [GQ ; V][k][d] (K = 32: 16 GQ rows, 16 source rows):
+//   dV^T[d][n]  = sum_k A[d][k] [alpha ; da ; diag(c)][k][n]
+//   dQ^T[d][s] += sum_k A[d][k] [0 ; da^T][k][s]            (over the tokens)
+// both v_mfma_f32_16x16x32 (on gfx950 the K = 16 form costs the same issue
+// time for half the work). A comes from two 4x4-transposed LDS reads. The fp32
+// coefficients are split into high and low 16-bit parts (two MFMAs each), so
 // dv keeps fp32-level error before its single rounding and dq accumulates in
 // fp32 registers for the whole kernel (one partial row per query and
 // workgroup, reduced afterwards in a fixed order).
@@ -410,37 +413,75 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
 // Layout of the D[n][c] result: lane (g, i) holds rows n = 4g + j of column
 // i, so lanes i and i ^ 8 hold G and the logit dot of query i & 7 (one DPP
 // row rotation swaps them); the softmax over n runs over j and the four
-// 16-lane groups. That is the B layout of the dq product (k = n, column s);
-// the dv product needs the transpose (k = coefficient, column n), which goes
-// through a 1 KiB LDS table per wave.
+// 16-lane groups. The B operands need other lane layouts (k = 8g + j, column
+// i), which go through two small LDS tables per wave.
 //
-// Work split as in the forward: 4 waves per workgroup, one token at a time,
-// wave w owns D/4 columns, each wave reads back only the LDS rows it wrote;
-// the logit partials cross the waves through LDS once per token. The next
-// token's v and g rows are loaded into registers while the current one is
-// computed. dv rows leave through LDS staging as SC-column row segments, all
-// rows of a store from one buffer resource ((n_src - 1) * stride + D*2 bytes
-// must stay below 2^31, checked by the host). Every global load and store in
-// the loop is unconditional (see k_batched_mx), so the waits are exact.
+// Work split as in the forward: W waves per workgroup (4, or 8 = two per
+// SIMD), one token at a time, wave w owns D/W columns and reads back only the
+// LDS rows it wrote; the logit partials cross the waves through LDS once per
+// token. The v and g rows of the token after next are loaded into registers
+// a few rows per output block of the current one (a burst of loads would
+// stall the wave at issue), and written to LDS when the next one is done; a
+// load covers 64 / (chunks of a wave's slice) rows. dv rows leave through LDS
+// staging as SC-column row segments, all rows of a store from one buffer
+// resource (offsets below 2^31, checked by the host). Every global load and
+// store in the loop is unconditional (see k_batched_mx), so the waits are
+// exact. The cross-lane sums of the softmax use the gfx950 row swaps
+// (v_permlane16/32_swap) instead of LDS-routed shuffles.
 //
 // Reference: the batched forward is src/switchyard/triton_op.py:378-501; it
 // has no backward (the single-query derivation is at :205-214).
-template <class T, int KS, int NR>
-__global__ void __launch_bounds__(256, 1)
+#ifndef SY_BMX_TWO_DEEP
+#define SY_BMX_TWO_DEEP 1
+#endif
+constexpr bool kBmxTwoDeep = SY_BMX_TWO_DEEP != 0;
+
+// Pair reductions over lanes (l, l ^ 16) and (l, l ^ 32) with the gfx950 row
+// swaps (VALU, no LDS round trip). Each swap leaves the even-row (low-half)
+// value in one result and the odd-row (high-half) value in the other, so every
+// lane combines the same two operands in the same order.
+__device__ __forceinline__ f32x2_t swap16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return f32x2_t{__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+__device__ __forceinline__ f32x2_t swap32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return f32x2_t{__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+__device__ __forceinline__ float sum64(float x) {  // over the four 16-lane groups
+  f32x2_t p = swap16(x);
+  p = swap32(p[0] + p[1]);
+  return p[0] + p[1];
+}
+__device__ __forceinline__ float max64(float x) {
+  f32x2_t p = swap16(x);
+  p = swap32(fmaxf(p[0], p[1]));
+  return fmaxf(p[0], p[1]);
+}
+
+template <class T, int KS, int NR, int W>
+__global__ void __launch_bounds__(64 * W, 1)
 k_bwd_batched_mx(const RowTable v, const uint16_t* __restrict__ q, const uint16_t* __restrict__ g,
                  const RowTable dv, float* __restrict__ partial, int n_src, int n_q,
                  int64_t n_tok, float eps, float inv_d) {
   using M = Mx<T>;
-  constexpr int d = 128 * KS;
+  constexpr int d = 32 * KS * W;
   constexpr uint32_t rs = (uint32_t)d * 2u + kMxPad;
   constexpr uint32_t row_bytes = (uint32_t)d * 2u;
-  constexpr int cpr = 4 * KS;
+  constexpr int cpr = 4 * KS;  // 16-byte chunks of a row in a wave's slice
   constexpr uint32_t kDrop = 0x80000000u;
   constexpr int SQ = (int)kBwdMatrixMaxQ;
   static_assert(SQ == 8, "g and q rows take 8 of the 16 MFMA columns each");
+  // Staging loads cover kRpl rows each (lane / cpr picks the row) when a
+  // wave's slice is narrower than 64 chunks.
+  constexpr int kRpl = cpr <= 32 && 64 % cpr == 0 ? 64 / cpr : 1;
+  constexpr int kVl = (NR + kRpl - 1) / kRpl;  // source-row loads
+  constexpr int kGl = (SQ + kRpl - 1) / kRpl;  // g-row loads
   // dv staging: SC columns per round, stride SC*2 + 16 bytes; a store covers
   // kRpi rows with kLpr lanes each.
-  constexpr int SC = NR <= 9 && KS % 8 == 0 ? 256 : 128;
+  constexpr int SC = bwd_matrix_store_cols(NR, KS, W);
   static_assert((32 * KS) % SC == 0, "store rounds must tile the wave's columns");
   constexpr int kRow = SC * 2 + 16;
   constexpr int kLpr = SC / 8;
@@ -450,10 +491,14 @@ k_bwd_batched_mx(const RowTable v, const uint16_t* __restrict__ q, const uint16_
   extern __shared__ __align__(16) char lds[];
   char* const gq = lds;            // 16 rows: g of the token, then the queries
   char* const vs = lds + 16 * rs;  // n_src source rows, then a zero row
-  __shared__ __align__(16) float xl[2][kMxWaves][64][4];
-  __shared__ __align__(16) float xs[2][kMxWaves][kMxRows];
-  __shared__ __align__(16) float tt[kMxWaves][16 * kTs];
-  __shared__ __align__(16) char ob[kMxWaves][kRounds * kRpi * kRow];
+  __shared__ __align__(16) float xl[2][W][64][4];
+  __shared__ __align__(16) float xs[2][W][kMxRows];
+  __shared__ __align__(16) float tt[W][16 * kTs];
+  __shared__ __align__(16) float ut[W][8 * kTs];
+  // Staged rows: the store rounds' rows plus row NR, where lanes of rows
+  // past n_src write (unconditional LDS writes, no branches).
+  constexpr int kObRows = kRounds * kRpi > NR ? kRounds * kRpi : NR + 1;
+  __shared__ __align__(16) char ob[W][kObRows * kRow];
 
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
@@ -462,9 +507,17 @@ k_bwd_batched_mx(const RowTable v, const uint16_t* __restrict__ q, const uint16_
   const int cb = w * 32 * KS;
   const uint32_t coff = lane < cpr ? (uint32_t)(cb + 8 * lane) * 2u : kDrop;
   const int loff = (cb + 8 * lane) * 2;  // this lane's chunk (bytes into a row)
+  // Staging: this lane's row within a load and its chunk.
+  const int lr = kRpl > 1 ? lane / cpr : 0;
+  const int lc = kRpl > 1 ? lane % cpr : lane;
+  const bool lane_ok = kRpl > 1 || lane < cpr;
+  const int soff = (cb + 8 * lc) * 2;
+  const uint32_t v_stride = (uint32_t)v.stride_bytes;
+  const uint32_t g_stride = (uint32_t)(n_tok * d * 2);
 
-  // Queries (GQ rows 8..15, zero past n_q) and the zero source row.
-  {
+  // Queries (GQ rows 8..15, zero past n_q) and the zero source row; called
+  // after the first token's loads are issued, so both arrive in one wait.
+  auto queries = [&]() {
     i32x4_t qv[SQ];
 #pragma unroll
     for (int s = 0; s < SQ; ++s)
@@ -474,7 +527,7 @@ k_bwd_batched_mx(const RowTable v, const uint16_t* __restrict__ q, const uint16_
       for (int s = 0; s < SQ; ++s) *(i32x4_t*)(gq + (8 + s) * rs + loff) = qv[s];
       *(i32x4_t*)(vs + n_src * rs + loff) = i32x4_t{0, 0, 0, 0};
     }
-  }
+  };
 
   f32x4_t qacc[KS / 2][4];
 #pragma unroll
@@ -486,32 +539,42 @@ k_bwd_batched_mx(const RowTable v, const uint16_t* __restrict__ q, const uint16_
   const int64_t first = blockIdx.x;
   const int iters = first < n_tok ? (int)((n_tok - first + step - 1) / step) : 0;
 
-  auto stage = [&](i32x4_t (&sv)[NR], i32x4_t (&sg)[SQ], int64_t t) {
+  // Staging load r of token t: source rows [r*kRpl, +kRpl) (r < kVl), else
+  // g rows [(r - kVl)*kRpl, +kRpl), one buffer resource per load (tokens past
+  // n_tok and missing rows load zeros without memory traffic).
+  constexpr int kLoads = kVl + kGl;
+  auto issue = [&](i32x4_t (&sv)[kVl], i32x4_t (&sg)[kGl], int64_t t, int r) {
     const bool tok_ok = t < n_tok;
     const int64_t tc = tok_ok ? t : n_tok - 1;
-#pragma unroll
-    for (int n = 0; n < NR; ++n) {
-      const bool real = n < n_src && tok_ok;
-      sv[n] = ld16_stream(make_rsrc(row_at<false, const uint16_t>(v, n < n_src ? n : 0) + tc * d,
-                                    real ? row_bytes : 0u),
-                          coff);
-    }
-#pragma unroll
-    for (int s = 0; s < SQ; ++s) {
-      const bool real = s < n_q && tok_ok;
-      sg[s] = ld16_stream(
-          make_rsrc(g + ((int64_t)(s < n_q ? s : 0) * n_tok + tc) * d, real ? row_bytes : 0u),
-          coff);
+    if (r < kVl) {
+      const int n0 = r * kRpl, n = n0 + lr;
+      const int last = (n_src < n0 + kRpl ? n_src : n0 + kRpl) - 1;  // last real row
+      const uint32_t bytes = tok_ok && n0 < n_src ? (uint32_t)(last - n0) * v_stride + row_bytes : 0u;
+      const auto rr = make_rsrc(row_at<false, const uint16_t>(v, n0 < n_src ? n0 : 0) + tc * d, bytes);
+      sv[r] = ld16_stream(rr, lane_ok && n < n_src ? (uint32_t)lr * v_stride + (uint32_t)soff : kDrop);
+    } else {
+      const int s0 = (r - kVl) * kRpl, s = s0 + lr;
+      const int last = (n_q < s0 + kRpl ? n_q : s0 + kRpl) - 1;
+      const uint32_t bytes = tok_ok && s0 < n_q ? (uint32_t)(last - s0) * g_stride + row_bytes : 0u;
+      const auto rr = make_rsrc(g + ((int64_t)(s0 < n_q ? s0 : 0) * n_tok + tc) * d, bytes);
+      sg[r - kVl] = ld16_stream(rr, lane_ok && s < n_q ? (uint32_t)lr * g_stride + (uint32_t)soff : kDrop);
     }
   };
-  auto commit = [&](const i32x4_t (&sv)[NR], const i32x4_t (&sg)[SQ]) {
+  auto stage = [&](i32x4_t (&sv)[kVl], i32x4_t (&sg)[kGl], int64_t t) {
+#pragma unroll
+    for (int r = 0; r < kLoads; ++r) issue(sv, sg, t, r);
+  };
+  // Rows past n_src hold zeros (dropped loads) and go to the zero row.
+  auto commit = [&](const i32x4_t (&sv)[kVl], const i32x4_t (&sg)[kGl]) {
     wave_lds_fence();
-    if (lane < cpr) {
+    if (lane_ok) {
 #pragma unroll
-      for (int n = 0; n < NR; ++n)
-        if (n < n_src) *(i32x4_t*)(vs + n * rs + loff) = sv[n];
+      for (int r = 0; r < kVl; ++r) {
+        const int n = r * kRpl + lr;
+        *(i32x4_t*)(vs + (n < n_src ? n : n_src) * rs + soff) = sv[r];
+      }
 #pragma unroll
-      for (int s = 0; s < SQ; ++s) *(i32x4_t*)(gq + s * rs + loff) = sg[s];
+      for (int r = 0; r < kGl; ++r) *(i32x4_t*)(gq + (r * kRpl + lr) * rs + soff) = sg[r];
     }
     wave_lds_fence();
   };
@@ -520,12 +583,16 @@ k_bwd_batched_mx(const RowTable v, const uint16_t* __restrict__ q, const uint16_
   const int ra = qi < n_src ? qi : n_src;
   const char* const abase = vs + ra * rs + (cb + 8 * grp) * 2;
   const char* const bbase = gq + qi * rs + (cb + 8 * grp) * 2;
-  // Transposed reads (A of both output products): row 4*grp + qi/4 of GQ and
-  // of V, at the forward's bank-conflict-free column pieces.
+  // Transposed reads (A of both output products, k = 8*grp + j): lane
+  // (grp, 4j + t) reads row k = 8*grp + j (first read) and 8*grp + 4 + j
+  // (second read), k < 16 from GQ, else V row k - 16 (the zero row past
+  // n_src), at the forward's bank-conflict-free column pieces t.
   const uint32_t toff = (uint32_t)cb * 2u + 8u * (qi & 1) + 64u * ((qi >> 1) & 1);
-  const int kt = 4 * grp + (qi >> 2);
-  const char* const tgq = gq + kt * rs + toff;
-  const char* const tvs = vs + (kt < n_src ? kt : n_src) * rs + toff;
+  auto trow = [&](int k) {
+    return k < 16 ? gq + k * rs : vs + (k - 16 < n_src ? k - 16 : n_src) * rs;
+  };
+  const char* const ta1 = trow(8 * grp + (qi >> 2)) + toff;
+  const char* const ta2 = trow(8 * grp + 4 + (qi >> 2)) + toff;
   auto tread = [&](const char* base, int b, int a) {
     return __builtin_bit_cast(i32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                                            (lds_s16x4_t*)(base + b * 128 + a * 16)));
@@ -533,14 +600,18 @@ k_bwd_batched_mx(const RowTable v, const uint16_t* __restrict__ q, const uint16_
   // Output layout of MFMA a of a 64-column block: lane (grp, qi) holds row n = qi
   // (dv) or query s = qi (dq) at local columns 8a + ocol + j, j < 4.
   const int ocol = 4 * (grp & 1) + 32 * (grp >> 1);
-  const char* const cvb = vs + ra * rs + (cb + ocol) * 2;
+  const int wrow = qi < n_src ? qi : NR;  // staging row of this lane's dv values
   float* const tw = tt[w];
+  float* const tu = ut[w];
   char* const obw = ob[w];
   const uint32_t dv_stride = (uint32_t)dv.stride_bytes;
   const uint32_t dv_bytes = (uint32_t)(n_src - 1) * dv_stride + row_bytes;
   const bool gl = qi < 8;  // column qi is G (else the logit dot of query qi - 8)
 
-  auto token = [&](int k, int64_t tok) {
+  // Token tok (exchange buffer k & 1); its output loop also issues the loads
+  // of token stok into (sv, sg), a few per block, so that no wave stalls on a
+  // burst of loads.
+  auto token = [&](int k, int64_t tok, i32x4_t (&sv)[kVl], i32x4_t (&sg)[kGl], int64_t stok) {
     // 1. D[n][c] partials over this wave's columns, and the sums of squares.
     constexpr int kAhead = 4;
     f32x4_t acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -571,8 +642,7 @@ k_bwd_batched_mx(const RowTable v, const uint16_t* __restrict__ q, const uint16_
     }
     const f32x4_t acc = acc0 + acc1;
     float ss = ss0 + ss1;
-    ss += __shfl_xor(ss, 16);
-    ss += __shfl_xor(ss, 32);
+    ss = sum64(ss);
     const int xb = k & 1;
     *(f32x4_t*)&xl[xb][w][lane][0] = acc;
     if (lane < kMxRows) xs[xb][w][lane] = ss;
@@ -580,7 +650,7 @@ k_bwd_batched_mx(const RowTable v, const uint16_t* __restrict__ q, const uint16_
     f32x4_t lt = *(const f32x4_t*)&xl[xb][0][lane][0];
     f32x4_t sq = *(const f32x4_t*)&xs[xb][0][4 * grp];
 #pragma unroll
-    for (int ww = 1; ww < kMxWaves; ++ww) {
+    for (int ww = 1; ww < W; ++ww) {
       lt += *(const f32x4_t*)&xl[xb][ww][lane][0];
       sq += *(const f32x4_t*)&xs[xb][ww][4 * grp];
     }
@@ -597,8 +667,7 @@ k_bwd_batched_mx(const RowTable v, const uint16_t* __restrict__ q, const uint16_
       lg[j] = 4 * grp + j < n_src ? lgr[j] : -INFINITY;
       mx = fmaxf(mx, lg[j]);
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = max64(mx);
     float p[4];
     int top = 64;  // first row at the maximum
 #pragma unroll
@@ -608,15 +677,14 @@ k_bwd_batched_mx(const RowTable v, const uint16_t* __restrict__ q, const uint16_
       if (real && lg[j] == mx) top = 4 * grp + j;
     }
     float ls = (p[0] + p[1]) + (p[2] + p[3]);
-    ls += __shfl_xor(ls, 16);
-    ls += __shfl_xor(ls, 32);
-    top = min(top, __shfl_xor(top, 16));
-    top = min(top, __shfl_xor(top, 32));
+    ls = sum64(ls);
+    // (row indices below 64 are exact in fp32)
+    top = (int)-max64(-(float)top);
     // G of the top row (lane (top / 4, qi), element top % 4): the dots are
     // taken relative to it, as in the single-query backward.
     const int tj = top & 3;
     const float gsel = tj == 0 ? G[0] : tj == 1 ? G[1] : tj == 2 ? G[2] : G[3];
-    const float gref = __shfl(gsel, ((top >> 2) & 3) * 16 + qi);
+    const float gref = sum64(grp == ((top >> 2) & 3) ? gsel : 0.0f);
     const float inv_l = 1.0f / ls;
     float al[4], dg[4];
     float sdev = 0.0f;
@@ -626,8 +694,7 @@ k_bwd_batched_mx(const RowTable v, const uint16_t* __restrict__ q, const uint16_
       dg[j] = G[j] - gref;
       sdev = fmaf(al[j], dg[j], sdev);
     }
-    sdev += __shfl_xor(sdev, 16);
-    sdev += __shfl_xor(sdev, 32);
+    sdev = sum64(sdev);
     float da[4], cn4[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -641,8 +708,13 @@ k_bwd_batched_mx(const RowTable v, const uint16_t* __restrict__ q, const uint16_
       cn4[j] = c;
     }
 
-    // 3. Coefficients of the dv product, transposed through LDS:
-    //    tw[n][k] = alpha[k][n] (k < 8), da[k - 8][n] (k >= 8); tw[n][16] = c_n.
+    // 3. B operands of the output products. The A operand of both is
+    //    A[d][k] (k < 32) = GQ[k][d] for k < 16, V[k - 16][d] for k >= 16;
+    //    lane (grp, i) supplies B[k = 8*grp + j][column i], j < 8.
+    //    dv:  B[k][n] = alpha[k][n], da[k - 8][n], then diag(c) (c_n v_n);
+    //    dq:  B[k][s] = 0 for the GQ rows, da[s][k - 16] for the V rows.
+    //    Tables (this wave's LDS): tw[n][k] = alpha[k][n] (k < 8),
+    //    da[k - 8][n] (k < 16), c_n (k = 16); tu[s][n] = da[s][n].
     wave_lds_fence();
 #pragma unroll
     for (int j = 0; j < 4; ++j) tw[(4 * grp + j) * kTs + qi] = gl ? al[j] : da[j];
@@ -650,35 +722,42 @@ k_bwd_batched_mx(const RowTable v, const uint16_t* __restrict__ q, const uint16_
 #pragma unroll
       for (int j = 0; j < 4; ++j) tw[(4 * grp + j) * kTs + 16] = cn4[j];
     }
+    *(f32x4_t*)&tu[(qi & 7) * kTs + 4 * grp] = f32x4_t{da[0], da[1], da[2], da[3]};
     wave_lds_fence();
-    const f32x4_t cf = *(const f32x4_t*)&tw[qi * kTs + 4 * grp];
     const float cn = tw[qi * kTs + 16];
-    const int c01 = M::pack2(cf[0], cf[1]), c23 = M::pack2(cf[2], cf[3]);
-    const i32x2_t ch = {c01, c23};
-    const i32x2_t cl = {M::pack2(cf[0] - M::lo(c01), cf[1] - M::hi(c01)),
-                        M::pack2(cf[2] - M::lo(c23), cf[3] - M::hi(c23))};
-    // B of the dq product: da[s = qi][n = 4*grp + j], columns 8..15 zero.
-    float db[4];
+    const f32x4_t w0 = *(const f32x4_t*)&tw[qi * kTs + 8 * (grp & 1)];
+    const f32x4_t w1 = *(const f32x4_t*)&tw[qi * kTs + 8 * (grp & 1) + 4];
+    const f32x4_t u0 = *(const f32x4_t*)&tu[(qi & 7) * kTs + 8 * (grp & 1)];
+    const f32x4_t u1 = *(const f32x4_t*)&tu[(qi & 7) * kTs + 8 * (grp & 1) + 4];
+    float bv[8], bq[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) db[j] = gl ? da[j] : 0.0f;
-    const int d01 = M::pack2(db[0], db[1]), d23 = M::pack2(db[2], db[3]);
-    const i32x2_t dh = {d01, d23};
-    const i32x2_t dlo = {M::pack2(db[0] - M::lo(d01), db[1] - M::hi(d01)),
-                         M::pack2(db[2] - M::lo(d23), db[3] - M::hi(d23))};
+    for (int j = 0; j < 8; ++j) {
+      const float wv = j < 4 ? w0[j] : w1[j - 4];
+      const float uv = j < 4 ? u0[j] : u1[j - 4];
+      bv[j] = grp < 2 ? wv : (8 * (grp & 1) + j == qi ? cn : 0.0f);
+      bq[j] = grp >= 2 && gl ? uv : 0.0f;
+    }
+    i32x4_t bvh, bvl, bqh, bql;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      bvh[j] = M::pack2(bv[2 * j], bv[2 * j + 1]);
+      bvl[j] = M::pack2(bv[2 * j] - M::lo(bvh[j]), bv[2 * j + 1] - M::hi(bvh[j]));
+      bqh[j] = M::pack2(bq[2 * j], bq[2 * j + 1]);
+      bql[j] = M::pack2(bq[2 * j] - M::lo(bqh[j]), bq[2 * j + 1] - M::hi(bqh[j]));
+    }
 
     // 4. dv (staged, SC columns per store round) and dq, 64 columns a block.
     constexpr int kBlocks = KS / 2;
     constexpr int kPerStage = SC / 64;
     const auto dr = make_rsrc(row_at<false, uint16_t>(dv, 0) + tok * d, dv_bytes);
-    // Operands of a block (A of both products, v for c_n v), read one block
-    // ahead of their MFMAs; scheduling barriers keep that window.
-    i32x2_t ag[2][4], av[2][4], vv[2][4];
+    // A operands of a block (k = 8*grp + j from two transposed reads), read
+    // one block ahead of their MFMAs; scheduling barriers keep that window.
+    i32x4_t aa[2][4];
     auto operands = [&](int b, int u) {
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
-        ag[u][a] = tread(tgq, b, a);
-        av[u][a] = tread(tvs, b, a);
-        vv[u][a] = *(const i32x2_t*)(cvb + (b * 64 + 8 * a) * 2);
+        const i32x2_t lo = tread(ta1, b, a), hi = tread(ta2, b, a);
+        aa[u][a] = i32x4_t{lo[0], lo[1], hi[0], hi[1]};
       }
     };
     operands(0, 0);
@@ -688,19 +767,16 @@ k_bwd_batched_mx(const RowTable v, const uint16_t* __restrict__ q, const uint16_
       if (b % kPerStage == 0) wave_lds_fence();
       if (b + 1 < kBlocks) operands(b + 1, u ^ 1);
 #pragma unroll
+      for (int r = b * kLoads / kBlocks; r < (b + 1) * kLoads / kBlocks; ++r) issue(sv, sg, stok, r);
+#pragma unroll
       for (int a = 0; a < 4; ++a) {
         f32x4_t c = {0.0f, 0.0f, 0.0f, 0.0f};
-        c = M::k16(ag[u][a], cl, c);
-        c = M::k16(ag[u][a], ch, c);
-        qacc[b][a] = M::k16(av[u][a], dlo, qacc[b][a]);
-        qacc[b][a] = M::k16(av[u][a], dh, qacc[b][a]);
-        const i32x2_t x = vv[u][a];
-        const float f0 = fmaf(cn, M::lo(x[0]), c[0]);
-        const float f1 = fmaf(cn, M::hi(x[0]), c[1]);
-        const float f2 = fmaf(cn, M::lo(x[1]), c[2]);
-        const float f3 = fmaf(cn, M::hi(x[1]), c[3]);
-        const i32x2_t o = {M::pack2(f0, f1), M::pack2(f2, f3)};
-        if (qi < n_src) *(i32x2_t*)(obw + qi * kRow + ((b % kPerStage) * 64 + 8 * a + ocol) * 2) = o;
+        c = M::k32(aa[u][a], bvl, c);
+        c = M::k32(aa[u][a], bvh, c);
+        qacc[b][a] = M::k32(aa[u][a], bql, qacc[b][a]);
+        qacc[b][a] = M::k32(aa[u][a], bqh, qacc[b][a]);
+        const i32x2_t o = {M::pack2(c[0], c[1]), M::pack2(c[2], c[3])};
+        *(i32x2_t*)(obw + wrow * kRow + ((b % kPerStage) * 64 + 8 * a + ocol) * 2) = o;
       }
       if (b % kPerStage == kPerStage - 1) {
         wave_lds_fence();
@@ -723,12 +799,23 @@ k_bwd_batched_mx(const RowTable v, const uint16_t* __restrict__ q, const uint16_
     }
   };
 
-  if (iters > 0) {
+  if (iters > 0 && !kBmxTwoDeep) {
+    // One staged token in flight while one is computed.
+    i32x4_t sva[kVl], sga[kGl];
+    stage(sva, sga, first);
+    queries();  // waits for the queries and the first token
+    commit(sva, sga);
+    for (int k = 0; k < iters; ++k) {
+      const int64_t tok = first + (int64_t)k * step;
+      token(k, tok, sva, sga, tok + step);
+      if (k + 1 < iters) commit(sva, sga);
+    }
+  } else if (iters > 0) {
     // Stores one token issues.
     constexpr int kTokenStores = (32 * KS / SC) * kRounds;
-    i32x4_t sva[NR], sga[SQ], svb[NR], sgb[SQ];
+    i32x4_t sva[kVl], sga[kGl], svb[kVl], sgb[kGl];
     stage(sva, sga, first);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): queries and the first token
+    queries();  // waits for the queries and the first token
     commit(sva, sga);
     stage(svb, sgb, first + step);
     // Dropped stores, so that the loads of the second set are followed by as
@@ -745,14 +832,13 @@ k_bwd_batched_mx(const RowTable v, const uint16_t* __restrict__ q, const uint16_
     int k = 0;
     for (; k + 1 < iters; k += 2) {
       const int64_t tok = first + (int64_t)k * step;
-      stage(sva, sga, tok + 2 * step);
-      token(k, tok);
+      token(k, tok, sva, sga, tok + 2 * step);
       commit(svb, sgb);
-      stage(svb, sgb, tok + 3 * step);
-      token(k + 1, tok + step);
+      token(k + 1, tok + step, svb, sgb, tok + 3 * step);
       if (k + 2 < iters) commit(sva, sga);
     }
-    if (k < iters) token(k, first + (int64_t)k * step);
+    // The odd last token stages nothing (its loads are past n_tok: dropped).
+    if (k < iters) token(k, first + (int64_t)k * step, sva, sga, n_tok);
   }
 
   // dq partial row of each query: partial[blockIdx][s][:].
@@ -819,10 +905,10 @@ hipError_t launch_mx_dtype(const BatchedArgs& a, hipStream_t s, KernelRes* info)
   }
 }
 
-template <class T, int KS, int NR>
+template <class T, int KS, int NR, int W>
 hipError_t launch_bmx(const BwdBatchedArgs& a, int grid, hipStream_t s, KernelRes* info) {
   const size_t lds = (size_t)bwd_matrix_dynamic_lds(a.n_src, a.d);
-  auto* kern = k_bwd_batched_mx<T, KS, NR>;
+  auto* kern = k_bwd_batched_mx<T, KS, NR, W>;
   KernelRes r{0, 0, 1, 0};
   static hipFuncAttributes fa;
   static const hipError_t fa_err =
@@ -831,8 +917,9 @@ hipError_t launch_bmx(const BwdBatchedArgs& a, int grid, hipStream_t s, KernelRe
   if (e != hipSuccess) return e;
   r.vgprs = fa.numRegs;
   r.lds = (int)(fa.sharedSizeBytes + lds);
+  if (r.lds > 160 * 1024) return hipErrorInvalidConfiguration;
   const int alloc = std::max(8, ((fa.numRegs + 7) / 8) * 8);
-  const int by_waves = std::min(8, 512 / alloc);  // one wave per SIMD per workgroup
+  const int by_waves = std::max(1, std::min(8, 512 / alloc) / (W / 4));  // waves per SIMD
   r.blocks_per_cu = std::max(1, std::min(by_waves, (160 * 1024) / std::max(1, r.lds)));
   int cus = 0;
   if (cu_count(&cus) != hipSuccess || cus < 1) cus = 1;
@@ -848,25 +935,39 @@ hipError_t launch_bmx(const BwdBatchedArgs& a, int grid, hipStream_t s, KernelRe
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kMxWaves), lds, s, a.v, (const uint16_t*)a.q,
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * W), lds, s, a.v, (const uint16_t*)a.q,
                      (const uint16_t*)a.g, a.dv, a.partial, a.n_src, a.n_q, a.n_tok, a.eps,
                      1.0f / (float)a.d);
   return hipGetLastError();
 }
 
-template <class T, int KS>
+template <class T, int KS, int W>
 hipError_t launch_bmx_rows(const BwdBatchedArgs& a, int grid, hipStream_t s, KernelRes* info) {
-  return a.n_src <= 9 ? launch_bmx<T, KS, 9>(a, grid, s, info)
-                      : launch_bmx<T, KS, 16>(a, grid, s, info);
+  if constexpr (32 * KS * W == 2048) {  // N <= 9 there (the 16-row tile spills)
+    return launch_bmx<T, KS, 9, W>(a, grid, s, info);
+  } else {
+    return a.n_src <= 9 ? launch_bmx<T, KS, 9, W>(a, grid, s, info)
+                        : launch_bmx<T, KS, 16, W>(a, grid, s, info);
+  }
 }
 
 template <class T>
 hipError_t launch_bmx_dtype(const BwdBatchedArgs& a, int grid, hipStream_t s, KernelRes* info) {
-  switch (a.d / 128) {
-    case 4: return launch_bmx_rows<T, 4>(a, grid, s, info);
-    case 8: return launch_bmx_rows<T, 8>(a, grid, s, info);
-    case 12: return launch_bmx_rows<T, 12>(a, grid, s, info);
-    case 16: return launch_bmx_rows<T, 16>(a, grid, s, info);
+  int w = bwd_matrix_waves(a.d);
+  // Measurement knob: four waves per workgroup where that tile exists.
+  if (const char* env = std::getenv("SY_BMX_WAVES")) w = std::atoi(env) == 4 ? 4 : w;
+  if (w == 8) {
+    switch (a.d) {
+      case 1024: return launch_bmx_rows<T, 4, 8>(a, grid, s, info);
+      case 2048: return launch_bmx_rows<T, 8, 8>(a, grid, s, info);
+      default: break;
+    }
+  }
+  switch (a.d) {
+    case 512: return launch_bmx_rows<T, 4, 4>(a, grid, s, info);
+    case 1024: return launch_bmx_rows<T, 8, 4>(a, grid, s, info);
+    case 1536: return launch_bmx_rows<T, 12, 4>(a, grid, s, info);
+    case 2048: return launch_bmx_rows<T, 16, 4>(a, grid, s, info);
     default: return hipErrorInvalidConfiguration;
   }
 }
@@ -876,7 +977,8 @@ hipError_t launch_bmx_dtype(const BwdBatchedArgs& a, int grid, hipStream_t s, Ke
 hipError_t launch_bwd_batched_matrix(const BwdBatchedArgs& a, int grid, hipStream_t s,
                                      KernelRes* info) {
   if (!bwd_matrix_fits(a.n_src, a.n_q, a.d, a.dtype)) return hipErrorInvalidConfiguration;
-  if (!bwd_matrix_offsets_fit(a.n_src, a.n_tok, a.d)) return hipErrorInvalidConfiguration;
+  if (!bwd_matrix_offsets_fit(a.n_src, a.n_tok, a.d, a.v.stride_bytes))
+    return hipErrorInvalidConfiguration;
   if (a.n_tok == 0) return hipSuccess;
   return a.dtype == SY_BF16 ? launch_bmx_dtype<BF16>(a, grid, s, info)
                             : launch_bmx_dtype<F16>(a, grid, s, info);
