@@ -431,11 +431,6 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
 //
 // Reference: the batched forward is src/switchyard/triton_op.py:378-501; it
 // has no backward (the single-query derivation is at :205-214).
-#ifndef SY_BMX_TWO_DEEP
-#define SY_BMX_TWO_DEEP 1
-#endif
-constexpr bool kBmxTwoDeep = SY_BMX_TWO_DEEP != 0;
-
 // Pair reductions over lanes (l, l ^ 16) and (l, l ^ 32) with the gfx950 row
 // swaps (VALU, no LDS round trip). Each swap leaves the even-row (low-half)
 // value in one result and the odd-row (high-half) value in the other, so every
@@ -799,18 +794,9 @@ k_bwd_batched_mx(const RowTable v, const uint16_t* __restrict__ q, const uint16_
     }
   };
 
-  if (iters > 0 && !kBmxTwoDeep) {
-    // One staged token in flight while one is computed.
-    i32x4_t sva[kVl], sga[kGl];
-    stage(sva, sga, first);
-    queries();  // waits for the queries and the first token
-    commit(sva, sga);
-    for (int k = 0; k < iters; ++k) {
-      const int64_t tok = first + (int64_t)k * step;
-      token(k, tok, sva, sga, tok + step);
-      if (k + 1 < iters) commit(sva, sga);
-    }
-  } else if (iters > 0) {
+  // Two staged tokens in flight while one is computed (one in flight measured
+  // the same at config 3: 115.4 vs 116.7 us).
+  if (iters > 0) {
     // Stores one token issues.
     constexpr int kTokenStores = (32 * KS / SC) * kRounds;
     i32x4_t sva[kVl], sga[kGl], svb[kVl], sgb[kGl];
