@@ -121,8 +121,8 @@ __device__ __forceinline__ void wave_lds_fence() {
 // theirs), so the number of memory operations between a prefetch and its use
 // is a compile-time constant and the compiler waits for exactly the prefetch,
 // not for everything in flight.
-template <class T, int KS, int NR, int SQ>
-__global__ void __launch_bounds__(256, 2)
+template <class T, int KS, int NR, int SQ, int TP>
+__global__ void __launch_bounds__(256 * TP, 2 / TP)
 k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restrict__ out,
              float* __restrict__ m_out, float* __restrict__ l_out, int normalize, int n_src,
              int n_q, int64_t n_tok, float eps, float inv_d) {
@@ -132,9 +132,9 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
   constexpr uint32_t row_bytes = (uint32_t)d * 2u;
   constexpr int cpr = 4 * KS;  // 16-byte chunks per row in a wave's slice (<= 64)
   constexpr uint32_t kDrop = 0x80000000u;  // store offset past every resource
-  extern __shared__ __align__(16) char vs[];
-  __shared__ __align__(16) float xl[2][kMxWaves][64][4];  // logit partials, C layout
-  __shared__ __align__(16) float xs[2][kMxWaves][kMxRows];  // sum-of-squares partials
+  extern __shared__ __align__(16) char vs_all[];
+  __shared__ __align__(16) float xl[2][TP][kMxWaves][64][4];  // logit partials, C layout
+  __shared__ __align__(16) float xs[2][TP][kMxWaves][kMxRows];  // sum-of-squares partials
   // Output staging: [query][SC columns] per wave (the MFMA result layout
   // gives each lane 8 bytes of one query).
   // 256-column rounds halve the store count; the 16-row staging leaves no
@@ -145,10 +145,15 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
   constexpr int kLpq = SC / 8;                        // lanes per query row
   constexpr int kQpi = 64 / kLpq;                     // query rows per store
   constexpr int kRounds = SQ / kQpi;
-  __shared__ __align__(16) char ob[kMxWaves][SQ * kRow];
+  __shared__ __align__(16) char ob[TP][kMxWaves][SQ * kRow];
 
   const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
+  // TP tokens per workgroup: waves 4h..4h+3 own token slot h (its own LDS
+  // rows and buffers); the slots of a workgroup advance in step (one barrier
+  // per token), so no co-resident slot runs ahead of another.
+  const int half = TP > 1 ? (int)(threadIdx.x >> 8) : 0;
+  const int w = (threadIdx.x >> 6) & 3;
+  char* const vs = vs_all + (size_t)half * (size_t)(n_src + 1) * rs;
   const int qi = lane & 15;  // MFMA column: query (logits, output) / row (A of logits)
   const int g = lane >> 4;   // 16-lane group
   const int cb = w * 32 * KS;  // first column of this wave
@@ -165,10 +170,15 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
   // Zero row (index n_src), this wave's slice.
   if (lane < cpr) *(i32x4_t*)(vs + n_src * rs + (cb + 8 * lane) * 2) = i32x4_t{0, 0, 0, 0};
 
+  // Persistent over groups of TP consecutive tokens; slot `half` takes token
+  // (group * TP + half), which is past n_tok only in an odd last group (its
+  // loads and stores are then dropped).
   const int64_t step = gridDim.x;
   const int64_t first = blockIdx.x;
-  const int iters = first < n_tok ? (int)((n_tok - first + step - 1) / step) : 0;
+  const int64_t n_groups = (n_tok + TP - 1) / TP;
+  const int iters = first < n_groups ? (int)((n_groups - first + step - 1) / step) : 0;
   if (iters == 0) return;  // uniform over the workgroup
+  auto tok_at = [&](int64_t k) { return (first + k * step) * TP + half; };
 
   // Staging: chunk `lane` of each row of this wave's slice of token t (rows
   // past n_src and tokens past n_tok load zeros through a zero-size resource).
@@ -235,15 +245,15 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
     ss += __shfl_xor(ss, 16);
     ss += __shfl_xor(ss, 32);
     const int xb = k & 1;
-    *(f32x4_t*)&xl[xb][w][lane][0] = acc;
-    if (lane < kMxRows) xs[xb][w][lane] = ss;
+    *(f32x4_t*)&xl[xb][half][w][lane][0] = acc;
+    if (lane < kMxRows) xs[xb][half][w][lane] = ss;
     __syncthreads();
     // Lane (g, qi) now holds rows n = 4g + j of query column s = qi.
     f32x4_t pl4[kMxWaves], ps4[kMxWaves];
 #pragma unroll
     for (int ww = 0; ww < kMxWaves; ++ww) {
-      pl4[ww] = *(const f32x4_t*)&xl[xb][ww][lane][0];
-      ps4[ww] = *(const f32x4_t*)&xs[xb][ww][4 * g];
+      pl4[ww] = *(const f32x4_t*)&xl[xb][half][ww][lane][0];
+      ps4[ww] = *(const f32x4_t*)&xs[xb][half][ww][4 * g];
     }
     f32x4_t lt = pl4[0], sq = ps4[0];
 #pragma unroll
@@ -282,7 +292,7 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
     // 8a + 4(g%2) + 32(g/2) + j, j < 4; it stages them (8 bytes) and every
     // SC columns the wave stores SC*2-byte row segments.
     const float inv_l = normalize ? 1.0f / ls : 1.0f;
-    char* obw = ob[w];
+    char* obw = ob[half][w];
     constexpr int kBlocks = KS / 2;            // 64-column blocks of this wave
     constexpr int kPerStage = SC / 64;         // blocks per store round
     auto tread = [&](int b, int a) {
@@ -323,7 +333,7 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
           vals[rr] = *(const i32x4_t*)(obw + (kQpi * rr + lane / kLpq) * kRow + chunk * 16);
 #pragma unroll
         for (int rr = 0; rr < kRounds; ++rr) {
-          const int live = n_q - kQpi * rr;  // queries of this round (may be <= 0)
+          const int live = tok < n_tok ? n_q - kQpi * rr : 0;  // queries of this round
           const uint32_t bytes =
               live <= 0 ? 0u
                         : (uint32_t)(live > kQpi ? kQpi - 1 : live - 1) * q_stride + row_bytes;
@@ -339,7 +349,8 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
     }
     const auto mr = make_rsrc(m_out, stat_bytes);
     const auto lr = make_rsrc(l_out, stat_bytes);
-    const uint32_t so = stat_lane ? (uint32_t)(((int64_t)qi * n_tok + tok) * 4) : kDrop;
+    const uint32_t so =
+        stat_lane && tok < n_tok ? (uint32_t)(((int64_t)qi * n_tok + tok) * 4) : kDrop;
     __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(mx), mr, so, 0, 0);
     __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(ls), lr, so, 0, 0);
   };
@@ -350,13 +361,13 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
   // not leave the registers for two staging sets.
   constexpr bool kTwoDeep = NR <= 9 || KS < 16;
   i32x4_t sa[NR], sb[kTwoDeep ? NR : 1];
-  stage(sa, first);
+  stage(sa, tok_at(0));
   // Queries and the first token have landed before the loop: the compiler
   // then knows no register of theirs is pending inside it.
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   commit(sa);
   if constexpr (kTwoDeep) {
-    stage(sb, first + step);
+    stage(sb, tok_at(1));
     // As many (dropped) stores as a token issues: entering the loop, the
     // loads of sb are then followed by the same number of memory operations
     // as on every later pass, so the compiler's wait before committing sb
@@ -371,20 +382,18 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
     __builtin_amdgcn_sched_barrier(0);
     for (int k = 0; k < iters; k += 2) {
       // Token k is in LDS, token k+1 in flight in sb.
-      const int64_t tok = first + (int64_t)k * step;
-      stage(sa, tok + 2 * step);
-      token(k, tok);
+      stage(sa, tok_at(k + 2));
+      token(k, tok_at(k));
       if (k + 1 >= iters) break;
       commit(sb);
-      stage(sb, tok + 3 * step);
-      token(k + 1, tok + step);
+      stage(sb, tok_at(k + 3));
+      token(k + 1, tok_at(k + 1));
       if (k + 2 < iters) commit(sa);
     }
   } else {
     for (int k = 0; k < iters; ++k) {
-      const int64_t tok = first + (int64_t)k * step;
-      stage(sa, tok + step);
-      token(k, tok);
+      stage(sa, tok_at(k + 1));
+      token(k, tok_at(k));
       if (k + 1 < iters) commit(sa);
     }
   }
@@ -839,10 +848,10 @@ k_bwd_batched_mx(const RowTable v, const uint16_t* __restrict__ q, const uint16_
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-template <class T, int KS, int NR, int SQ>
+template <class T, int KS, int NR, int SQ, int TP>
 hipError_t launch_mx(const BatchedArgs& a, hipStream_t s, KernelRes* info) {
-  const size_t lds = (size_t)(a.n_src + 1) * ((size_t)a.d * 2 + kMxPad);
-  auto* kern = k_batched_mx<T, KS, NR, SQ>;
+  const size_t lds = (size_t)TP * (size_t)(a.n_src + 1) * ((size_t)a.d * 2 + kMxPad);
+  auto* kern = k_batched_mx<T, KS, NR, SQ, TP>;
   KernelRes r{0, 0, 1, 0};
   // The attributes of an instantiation do not change: query them once.
   static hipFuncAttributes fa;
@@ -852,12 +861,14 @@ hipError_t launch_mx(const BatchedArgs& a, hipStream_t s, KernelRes* info) {
   if (e != hipSuccess) return e;
   r.vgprs = fa.numRegs;
   r.lds = (int)(fa.sharedSizeBytes + lds);
+  if (r.lds > 160 * 1024) return hipErrorInvalidConfiguration;
   const int alloc = std::max(8, ((fa.numRegs + 7) / 8) * 8);
-  const int by_waves = std::min(8, 512 / alloc);  // one wave per SIMD per workgroup
+  const int by_waves = std::max(1, std::min(8, 512 / alloc) / TP);  // TP waves per SIMD
   r.blocks_per_cu = std::max(1, std::min(by_waves, (160 * 1024) / std::max(1, r.lds)));
   int cus = 0;
   if (cu_count(&cus) != hipSuccess || cus < 1) cus = 1;
-  r.grid = (int)std::max<int64_t>(1, std::min<int64_t>((int64_t)cus * r.blocks_per_cu, a.n_tok));
+  r.grid = (int)std::max<int64_t>(
+      1, std::min<int64_t>((int64_t)cus * r.blocks_per_cu, (a.n_tok + TP - 1) / TP));
   if (info != nullptr) {
     *info = r;
     return hipSuccess;
@@ -867,17 +878,37 @@ hipError_t launch_mx(const BatchedArgs& a, hipStream_t s, KernelRes* info) {
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(kern, dim3(r.grid), dim3(64 * kMxWaves), lds, s, a.v, (const uint16_t*)a.q,
+  hipLaunchKernelGGL(kern, dim3(r.grid), dim3(64 * kMxWaves * TP), lds, s, a.v,
+                     (const uint16_t*)a.q,
                      (uint16_t*)a.out, a.m_out, a.l_out, a.normalize, a.n_src, a.n_q, a.n_tok,
                      a.eps, 1.0f / (float)a.d);
   return hipGetLastError();
 }
 
+// Two token slots per workgroup at D = 2048 with N <= 9 (else one slot per
+// workgroup, two workgroups per CU). With two workgroups per CU the second one
+// to start falls behind (config 3 on MI355X: its workgroups end 9 us later on
+// average and the last ones 26 us after the first) and the CU runs half empty
+// until it catches up; two slots in step: 61.2 vs 72.8 us at config 3, 112.6 vs
+// 118.4 us at T = 8192. At smaller D or with 16 rows they are slower (D = 1024:
+// 39.2 vs 36.8 us; N=16 D=1536 S=16: 111.7 vs 85.0; N=5 D=512 S=6: 23.9 vs 19.3).
+template <class T, int KS, int NR, int SQ>
+hipError_t launch_mx_slots(const BatchedArgs& a, hipStream_t s, KernelRes* info) {
+  const char* env = std::getenv("SY_MX_SLOTS");  // measurement knob: 1 or 2 slots
+  const int want = env != nullptr ? std::atoi(env) : (KS == 16 && NR <= 9 ? 2 : 1);
+  KernelRes two;
+  if (want == 2 && launch_mx<T, KS, NR, SQ, 2>(a, s, &two) == hipSuccess)
+    return launch_mx<T, KS, NR, SQ, 2>(a, s, info);
+  return launch_mx<T, KS, NR, SQ, 1>(a, s, info);
+}
+
 template <class T, int KS>
 hipError_t launch_mx_rows(const BatchedArgs& a, hipStream_t s, KernelRes* info) {
   if (a.n_q <= 8)
-    return a.n_src <= 9 ? launch_mx<T, KS, 9, 8>(a, s, info) : launch_mx<T, KS, 16, 8>(a, s, info);
-  return a.n_src <= 9 ? launch_mx<T, KS, 9, 16>(a, s, info) : launch_mx<T, KS, 16, 16>(a, s, info);
+    return a.n_src <= 9 ? launch_mx_slots<T, KS, 9, 8>(a, s, info)
+                        : launch_mx_slots<T, KS, 16, 8>(a, s, info);
+  return a.n_src <= 9 ? launch_mx_slots<T, KS, 9, 16>(a, s, info)
+                      : launch_mx_slots<T, KS, 16, 16>(a, s, info);
 }
 
 template <class T>
