@@ -467,8 +467,8 @@ def sweep_mode(args):
         for s in sets:  # warm-up: a shape's first launches query kernel attributes
             fwd(s)
             bwd(s)
-        f_ms = harness.time_loop([lambda s=s: fwd(s) for s in sets], device=dev, iters=iters)
-        fb_ms = harness.time_loop([lambda s=s: (fwd(s), bwd(s)) for s in sets], device=dev, iters=iters)
+        f_ms = harness.time_loop_median([lambda s=s: fwd(s) for s in sets], device=dev, iters=iters)
+        fb_ms = harness.time_loop_median([lambda s=s: (fwd(s), bwd(s)) for s in sets], device=dev, iters=iters)
         fb = attn_res_train_bytes(n, b, t, d, item)
         fw = attn_res_min_bytes(n, b, t, d, item)
         fplan = _lib.plan(_lib.OP_FWD, n, d, dt)
@@ -502,7 +502,7 @@ def sweep_mode(args):
 
     for s in sets:  # warm-up: first launches load code objects and query attributes
         batched(s)
-    ms = harness.time_loop([lambda s=s: batched(s) for s in sets], device=dev, iters=100)
+    ms = harness.time_loop_median([lambda s=s: batched(s) for s in sets], device=dev, iters=100)
     nbytes = attn_res_batched_bytes(n, q, b, t, d, item)
     rec = {"sweep": "batched", "impl": "switchyard_hip", "N": n, "B": b, "T": t, "D": d, "Q": q, "dtype": tag,
            "fwd_us": round(ms * 1e3, 2), "fwd_gbps": round(nbytes / ms / 1e6, 1),
@@ -547,7 +547,7 @@ def schedule_mode(args):
     def timed(fns, iters=100):
         for f in fns:
             f()
-        return harness.time_loop(fns, device=dev, iters=iters)
+        return harness.time_loop_median(fns, device=dev, iters=iters)
 
     # --- pointer table vs stacked (config 2) ---------------------------------
     ws_bytes = int(lib.sy_bwd_workspace_bytes(n, nt, d, code, code))

@@ -114,6 +114,16 @@ def time_loop(fns: list[Callable[[], object]], *, device: torch.device, iters: i
     return start.elapsed_time(end) / iters
 
 
+def time_loop_median(fns: list[Callable[[], object]], *, device: torch.device, iters: int, reps: int = 3) -> float:
+    """Median over ``reps`` of :func:`time_loop`, after one untimed loop of
+    the same length: a few launches do not bring the device to its
+    sustained clocks (a batched forward's first 50-call loop reads ~6% slower
+    than its later ones)."""
+    time_loop(fns, device=device, iters=iters)
+    runs = sorted(time_loop(fns, device=device, iters=iters) for _ in range(reps))
+    return runs[len(runs) // 2]
+
+
 @dataclass
 class MemoryReport:
     peak_allocated_bytes: int
