@@ -446,17 +446,25 @@ __global__ void __launch_bounds__(256) k_probe_write(i32x4_t* __restrict__ dst, 
     __builtin_nontemporal_store(z, dst + i);
 }
 
+// Copy probe: each workgroup moves 16 KiB per step (four 16-byte loads per
+// thread, all issued before the stores), streamed both ways like the
+// operator's kernels; the buffer resources clip the last step to the buffer.
+// On MI355X this reaches ~6.0 TB/s (read + write) on 1 GiB, against ~5.4 TB/s
+// for a grid-stride loop with two loads in flight per thread.
 __global__ void __launch_bounds__(256)
-k_probe_copy(const i32x4_t* __restrict__ src, i32x4_t* __restrict__ dst, int64_t n16) {
-  const int64_t stride = (int64_t)gridDim.x * 256;
-  int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  for (; i + stride < n16; i += 2 * stride) {
-    const i32x4_t a = __builtin_nontemporal_load(src + i);
-    const i32x4_t b = __builtin_nontemporal_load(src + i + stride);
-    __builtin_nontemporal_store(a, dst + i);
-    __builtin_nontemporal_store(b, dst + i + stride);
+k_probe_copy(const char* __restrict__ src, char* __restrict__ dst, int64_t bytes) {
+  constexpr int64_t kChunk = 256 * 16 * 4;
+  for (int64_t base = (int64_t)blockIdx.x * kChunk; base < bytes;
+       base += (int64_t)gridDim.x * kChunk) {
+    const uint32_t len = (uint32_t)(bytes - base < kChunk ? bytes - base : kChunk);
+    const auto r = make_rsrc(src + base, len);
+    const auto w = make_rsrc(dst + base, len);
+    i32x4_t x[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) x[u] = ld16_stream(r, (threadIdx.x + 256u * u) * 16u);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) st16_stream(w, (threadIdx.x + 256u * u) * 16u, x[u]);
   }
-  for (; i < n16; i += stride) dst[i] = src[i];
 }
 
 }  // namespace
@@ -511,8 +519,8 @@ hipError_t launch_probe(int kind, const void* src, void* dst, int64_t bytes, int
   } else if (kind == 1) {
     hipLaunchKernelGGL(k_probe_write, dim3(grid), dim3(256), 0, s, (i32x4_t*)dst, n16);
   } else {
-    hipLaunchKernelGGL(k_probe_copy, dim3(grid), dim3(256), 0, s, (const i32x4_t*)src,
-                       (i32x4_t*)dst, n16);
+    hipLaunchKernelGGL(k_probe_copy, dim3(grid), dim3(256), 0, s, (const char*)src, (char*)dst,
+                       bytes);
   }
   return hipGetLastError();
 }
