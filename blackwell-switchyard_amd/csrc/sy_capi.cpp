@@ -63,6 +63,43 @@ int bwd_grid(const sy_plan& p, int64_t n_tok, int dtype, bool stats, int variant
   return SY_OK;
 }
 
+// Partial rows the backward's workspace provides: the largest persistent
+// grid of the vector plans (every variant, with and without forward stats).
+// A call whose buffers are not 16-byte aligned runs the generic kernel, which
+// is persistent over tokens at any grid and is capped to this count, so the
+// workspace is sized by the vector plans alone (2 MiB instead of 8 at N=9,
+// D=2048 on 256 CUs).
+int workspace_rows(int64_t n_src, int64_t n_tok, int64_t d, int v_dtype, int w_dtype, int* rows) {
+  int g = 0;
+  for (bool st : {true, false}) {
+    sy_plan p;
+    int rc = make_plan(SY_OP_BWD, n_src, 0, d, v_dtype, w_dtype, 1, &p, st);
+    if (rc != SY_OK) return rc;
+    apply_tile_override(SY_OP_BWD, n_src, d, &p);
+    for (int var : {0, 1, 2}) {
+      int gi = 0;
+      rc = bwd_grid(p, n_tok, v_dtype, st, var, &gi);
+      if (rc != SY_OK) return rc;
+      if (gi > g) g = gi;
+    }
+  }
+  *rows = g;
+  return SY_OK;
+}
+
+// The backward's grid for plan p: bwd_grid, capped to workspace_rows for the
+// generic kernel.
+int bwd_grid_for(const sy_plan& p, int64_t n_src, int64_t n_tok, int64_t d, int v_dtype,
+                 int w_dtype, bool stats, int variant, int* grid) {
+  int rc = bwd_grid(p, n_tok, v_dtype, stats, variant, grid);
+  if (rc != SY_OK || p.family != SY_FAMILY_GENERIC) return rc;
+  int rows = 0;
+  rc = workspace_rows(n_src, n_tok, d, v_dtype, w_dtype, &rows);
+  if (rc != SY_OK) return rc;
+  if (*grid > rows) *grid = rows;
+  return SY_OK;
+}
+
 // Plan of the batched backward for this token count: the matrix-core kernel
 // only where its dv offsets fit.
 int bwd_batched_plan(int64_t n_src, int64_t n_q, int64_t n_tok, int64_t d, int dtype, int aligned,
@@ -235,7 +272,7 @@ int bwd_main_impl(const RowTable& v, bool v_ok, const void* w, const void* g, co
   apply_tile_override(SY_OP_BWD, n_src, d, &p);
   int grid = 0;
   const int variant = listed ? 1 : (gm != nullptr ? 2 : 0);
-  rc = bwd_grid(p, n_tok, v_dtype, stats != nullptr, variant, &grid);
+  rc = bwd_grid_for(p, n_src, n_tok, d, v_dtype, w_dtype, stats != nullptr, variant, &grid);
   if (rc != SY_OK) return rc;
   if (workspace == nullptr || workspace_bytes < (int64_t)grid * d * (int64_t)sizeof(float))
     return SY_ERR_WORKSPACE;
@@ -380,25 +417,10 @@ int64_t sy_bwd_workspace_bytes(int64_t n_src, int64_t n_tok, int64_t d, int v_dt
   int rc = check_sizes(n_src, n_tok, d, v_dtype, w_dtype);
   if (rc != SY_OK) return rc;
   if (n_tok == 0) return 0;
-  // The vector plan assumes aligned buffers (a misaligned call falls back to
-  // the generic kernel with its own grid) and may depend on whether stats are
-  // passed, so size for the largest grid of every plan and variant.
-  int64_t g = 0;
-  for (int aligned : {1, 0}) {
-    for (bool st : {true, false}) {
-      sy_plan p;
-      rc = make_plan(SY_OP_BWD, n_src, 0, d, v_dtype, w_dtype, aligned, &p, st);
-      if (rc != SY_OK) return rc;
-      if (aligned) apply_tile_override(SY_OP_BWD, n_src, d, &p);
-      for (int var : {0, 1, 2}) {
-        int gi = 0;
-        rc = bwd_grid(p, n_tok, v_dtype, st, var, &gi);
-        if (rc != SY_OK) return rc;
-        if (gi > g) g = gi;
-      }
-    }
-  }
-  return g * d * (int64_t)sizeof(float);
+  int rows = 0;
+  rc = workspace_rows(n_src, n_tok, d, v_dtype, w_dtype, &rows);
+  if (rc != SY_OK) return rc;
+  return rows * d * (int64_t)sizeof(float);
 }
 
 int sy_bwd(const void* v, const void* w, const void* grad_out, const float* stats, void* dv,
@@ -480,7 +502,7 @@ int64_t sy_bwd_partial_rows(int64_t n_src, int64_t n_tok, int64_t d, int v_dtype
   if (rc != SY_OK) return rc;
   apply_tile_override(SY_OP_BWD, n_src, d, &p);
   int grid = 0;
-  rc = bwd_grid(p, n_tok, v_dtype, has_stats != 0, 0, &grid);
+  rc = bwd_grid_for(p, n_src, n_tok, d, v_dtype, w_dtype, has_stats != 0, 0, &grid);
   return rc != SY_OK ? rc : grid;
 }
 

@@ -142,3 +142,34 @@ def test_graph_replays_match_eager(dtype):
         torch.cuda.synchronize()
         assert torch.equal(dv, edv), f"replay {rep}: dv"
         assert torch.equal(dw, edw), f"replay {rep}: dw"
+
+
+def test_misaligned_buffers_fit_the_queried_workspace():
+    """v and dv one element past 16-byte alignment run the generic backward,
+    whose grid is capped to the partial rows sy_bwd_workspace_bytes sizes for
+    the vector plans; dv and dw still match the float64 oracle."""
+    n, t, d = 9, 1000, 2048
+    lib = _lib.lib()
+    v, w, go = _inputs(n, t, d, seed=11)
+    vbuf = torch.empty(v.numel() + 1, device=DEV, dtype=v.dtype)
+    vm = vbuf[1:].view(v.shape)
+    vm.copy_(v)
+    dvbuf = torch.empty_like(vbuf)
+    dv = dvbuf[1:].view(v.shape)
+    dw = torch.empty(d, device=DEV, dtype=w.dtype)
+    code = _lib.dtype_code(v.dtype)
+    ws = _workspace(n, t, d, v.dtype)
+    rows_vec = lib.sy_bwd_partial_rows(n, t, d, code, code, 1, 0)
+    rows_generic = lib.sy_bwd_partial_rows(n, t, d, code, code, 0, 0)
+    assert 1 <= rows_generic <= ws.numel() // d and rows_vec <= ws.numel() // d
+    rc = lib.sy_bwd(P(vm.data_ptr()), P(w.data_ptr()), P(go.data_ptr()), None, P(dv.data_ptr()),
+                    P(dw.data_ptr()), P(ws.data_ptr()), ws.numel() * 4, n, t, d, t * d, code, code, 1e-6,
+                    _lib.stream_ptr(v.device))
+    assert rc == 0
+    torch.cuda.synchronize()
+    rdv, rdw = c_oracle.backward(v[:, 0].double().cpu().numpy(), w.double().cpu().numpy(),
+                                 go[0].double().cpu().numpy())
+    for got, ref, what in ((dv[:, 0].cpu(), rdv, "dv"), (dw.cpu(), rdw, "dw")):
+        ref = torch.as_tensor(ref)
+        err = rel_l2(got, ref)
+        assert err <= 1.10 * dtype_floor(ref, torch.bfloat16), f"{what}: rel_l2 {err:.3e}"
