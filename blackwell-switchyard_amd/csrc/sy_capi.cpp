@@ -147,6 +147,19 @@ int bwd_batched_grid(const sy_plan& p, int64_t n_src, int64_t n_q, int64_t n_tok
   return SY_OK;
 }
 
+// Partial-row groups sy_bwd_batched_workspace_bytes provides: the grid of the
+// plan an aligned call takes when the matrix kernel's offsets fit. The other
+// plans (a source stride past the matrix kernel's 32-bit offsets, misaligned
+// buffers) are persistent over tokens at any grid and are capped to it.
+int batched_workspace_rows(int64_t n_src, int64_t n_q, int64_t n_tok, int64_t d, int dtype,
+                           int* rows) {
+  sy_plan p;
+  const int rc = make_plan(SY_OP_BWD_BATCHED, n_src, n_q, d, dtype, dtype, 1, &p, 1, 1);
+  if (rc != SY_OK) return rc;
+  return bwd_batched_grid(p, n_src, n_q, n_tok, d, dtype, rows);
+}
+
+
 hipError_t fwd_vec(const sy_plan& p, const FwdArgs& a, hipStream_t s) {
   if (a.v_dtype == SY_BF16) return launch_fwd_vec_bf16(p, a, s, nullptr);
   if (a.v_dtype == SY_F16) return launch_fwd_vec_f16(p, a, s, nullptr);
@@ -598,20 +611,10 @@ int64_t sy_bwd_batched_workspace_bytes(int64_t n_src, int64_t n_q, int64_t n_tok
   if (rc != SY_OK) return rc;
   if (n_q < 1 || n_q > 0x7fffffff) return SY_ERR_SHAPE;
   if (n_tok == 0) return 0;
-  int64_t g = 0;
-  // Every plan sy_bwd_batched may pick (it depends on alignment and, for the
-  // matrix kernel, on the source stride).
-  for (int aligned : {1, 0}) {
-    for (int matrix_ok : {1, 0}) {
-      sy_plan p;
-      rc = make_plan(SY_OP_BWD_BATCHED, n_src, n_q, d, dtype, dtype, aligned, &p, 1, matrix_ok);
-      if (rc != SY_OK) return rc;
-      int gi = 0;
-      rc = bwd_batched_grid(p, n_src, n_q, n_tok, d, dtype, &gi);
-      if (rc != SY_OK) return rc;
-      if (gi > g) g = gi;
-    }
-  }
+  int rows = 0;
+  rc = batched_workspace_rows(n_src, n_q, n_tok, d, dtype, &rows);
+  if (rc != SY_OK) return rc;
+  const int64_t g = rows;
   return g * n_q * d * (int64_t)sizeof(float);
 }
 
@@ -639,6 +642,10 @@ int sy_bwd_batched(const void* v, const void* queries, const void* grad_out, voi
   if (n_tok != 0) {
     rc = bwd_batched_grid(p, n_src, n_q, n_tok, d, dtype, &grid);
     if (rc != SY_OK) return rc;
+    int cap = 0;
+    rc = batched_workspace_rows(n_src, n_q, n_tok, d, dtype, &cap);
+    if (rc != SY_OK) return rc;
+    if (grid > cap) grid = cap;
     if (workspace == nullptr || workspace_bytes < (int64_t)grid * n_q * d * (int64_t)sizeof(float))
       return SY_ERR_WORKSPACE;
     const BwdBatchedArgs a{tv,         queries,    grad_out, td,     (float*)workspace,

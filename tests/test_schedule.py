@@ -329,6 +329,39 @@ def test_batched_backward_matrix_kernel(nstd, dtype):
         _close(qq.grad.cpu(), rdq, dtype, what="dq")
 
 
+def test_batched_backward_with_misaligned_queries_fits_the_queried_workspace():
+    """Queries one element past 16-byte alignment run the generic batched
+    backward, whose grid is capped to the partial rows
+    sy_bwd_batched_workspace_bytes sizes for the matrix kernel."""
+    import ctypes
+
+    n, s, t, d = 9, 8, 700, 2048
+    dtype = torch.bfloat16
+    v, _ = _make(n, t, d, dtype, seed=41)
+    gen = torch.Generator().manual_seed(42)
+    q = (torch.randn(s, d, generator=gen) * 2.0 / d**0.5).to(dtype).to(DEV)
+    g = torch.randn(s, 1, t, d, generator=gen).to(dtype).to(DEV)
+    qbuf = torch.empty(s * d + 1, device=DEV, dtype=dtype)
+    qm = qbuf[1:].view(s, d)
+    qm.copy_(q)
+    lib = _lib.lib()
+    code = _lib.dtype_code(dtype)
+    ws_bytes = lib.sy_bwd_batched_workspace_bytes(n, s, t, d, code)
+    assert ws_bytes > 0
+    ws = torch.empty(ws_bytes // 4, device=DEV)
+    dv = torch.empty_like(v)
+    dq = torch.empty(s, d, device=DEV, dtype=dtype)
+    P = ctypes.c_void_p
+    rc = lib.sy_bwd_batched(P(v.data_ptr()), P(qm.data_ptr()), P(g.data_ptr()), P(dv.data_ptr()),
+                            P(dq.data_ptr()), P(ws.data_ptr()), ws_bytes, n, s, t, d, t * d, code, 1e-6,
+                            _lib.stream_ptr(v.device))
+    assert rc == 0
+    torch.cuda.synchronize()
+    rdv, rdq = c_oracle.batched_backward(_np(v)[:, 0], _np(q), _np(g)[:, 0])
+    _close(dv[:, 0].cpu(), rdv, dtype, what="dv")
+    _close(dq.cpu(), rdq, dtype, what="dq")
+
+
 def test_batched_backward_is_deterministic_and_single_query_consistent():
     v, w = _make(9, 128, 2048, torch.bfloat16, seed=13)
     g = torch.randn(1, 1, 128, 2048, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).to(DEV)
