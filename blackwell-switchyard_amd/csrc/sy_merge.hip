@@ -8,6 +8,10 @@
 // One wavefront per token; lanes stride over the row in 16-byte chunks when
 // every row start is 16-byte aligned, element by element otherwise. HBM-bound
 // element-wise work: 2 row reads + 1 row write forward, 3 reads + 2 writes back.
+// Loads are streamed (non-temporal); stores take the default write-back
+// policy, unlike the operator's kernels: on MI355X at 4096 x 2048 bf16 the
+// gradient runs in 15.6-15.8 us against 17.1-17.4 us with streamed stores
+// (forward 10.5 against 10.6-11.0 us).
 #include <algorithm>
 
 #include "sy_device.hpp"
@@ -43,7 +47,7 @@ k_merge(const void* __restrict__ o1, const float* __restrict__ m1, const float* 
         float f[CE];
 #pragma unroll
         for (int e = 0; e < CE; ++e) f[e] = fmaf(s1, elem<T>(x, e), s2 * elem<T>(y, e));
-        st16_stream(ro, off, pack<T>(f));
+        st16(ro, off, pack<T>(f));
       }
     } else {
       for (int k = lane; k < d; k += 64) {
@@ -95,8 +99,8 @@ k_merge_bwd(const void* __restrict__ o1, const float* __restrict__ m1, const flo
           f1[e] = s1 * ge;
           f2[e] = s2 * ge;
         }
-        st16_stream(w1, off, pack<T>(f1));
-        st16_stream(w2, off, pack<T>(f2));
+        st16(w1, off, pack<T>(f1));
+        st16(w2, off, pack<T>(f2));
       }
     } else {
       for (int k = lane; k < d; k += 64) {
