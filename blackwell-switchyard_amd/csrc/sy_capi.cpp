@@ -75,7 +75,7 @@ int workspace_rows(int64_t n_src, int64_t n_tok, int64_t d, int v_dtype, int w_d
     sy_plan p;
     int rc = make_plan(SY_OP_BWD, n_src, 0, d, v_dtype, w_dtype, 1, &p, st);
     if (rc != SY_OK) return rc;
-    apply_tile_override(SY_OP_BWD, n_src, d, &p);
+    apply_tile_rules(SY_OP_BWD, n_src, n_tok, d, &p);
     for (int var : {0, 1, 2}) {
       int gi = 0;
       rc = bwd_grid(p, n_tok, v_dtype, st, var, &gi);
@@ -263,7 +263,7 @@ int fwd_impl(const RowTable& v, bool v_ok, const void* w, void* out, float* stat
   sy_plan p;
   const int rc = make_plan(SY_OP_FWD, n_src, 0, d, v_dtype, w_dtype, aligned, &p);
   if (rc != SY_OK) return rc;
-  apply_tile_override(SY_OP_FWD, n_src, d, &p);
+  apply_tile_rules(SY_OP_FWD, n_src, n_tok, d, &p);
   if (n_tok == 0) return SY_OK;
   const FwdArgs a{v,      w,       out,     stats,   m_out, l_out, normalize, (int)n_src,
                   n_tok,  (int)d,  v_dtype, w_dtype, eps};
@@ -282,7 +282,7 @@ int bwd_main_impl(const RowTable& v, bool v_ok, const void* w, const void* g, co
   sy_plan p;
   int rc = make_plan(SY_OP_BWD, n_src, 0, d, v_dtype, w_dtype, aligned, &p, stats != nullptr);
   if (rc != SY_OK) return rc;
-  apply_tile_override(SY_OP_BWD, n_src, d, &p);
+  apply_tile_rules(SY_OP_BWD, n_src, n_tok, d, &p);
   int grid = 0;
   const int variant = listed ? 1 : (gm != nullptr ? 2 : 0);
   rc = bwd_grid_for(p, n_src, n_tok, d, v_dtype, w_dtype, stats != nullptr, variant, &grid);
@@ -513,7 +513,7 @@ int64_t sy_bwd_partial_rows(int64_t n_src, int64_t n_tok, int64_t d, int v_dtype
   sy_plan p;
   rc = make_plan(SY_OP_BWD, n_src, 0, d, v_dtype, w_dtype, aligned, &p, has_stats != 0);
   if (rc != SY_OK) return rc;
-  apply_tile_override(SY_OP_BWD, n_src, d, &p);
+  apply_tile_rules(SY_OP_BWD, n_src, n_tok, d, &p);
   int grid = 0;
   rc = bwd_grid_for(p, n_src, n_tok, d, v_dtype, w_dtype, has_stats != 0, 0, &grid);
   return rc != SY_OK ? rc : grid;
@@ -528,7 +528,7 @@ int sy_kernel_info(int op, int64_t n_src, int64_t n_tok, int64_t d, int v_dtype,
   sy_plan p;
   rc = make_plan(op, n_src, 0, d, v_dtype, w_dtype, 1, &p);
   if (rc != SY_OK) return rc;
-  apply_tile_override(op, n_src, d, &p);
+  apply_tile_rules(op, n_src, n_tok, d, &p);
   out[0] = out[1] = out[2] = out[3] = 0;
   if (p.family == SY_FAMILY_GENERIC) return SY_OK;
   KernelRes r{0, 0, 0, 0};

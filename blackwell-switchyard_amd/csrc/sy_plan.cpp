@@ -245,4 +245,33 @@ void apply_tile_override(int op, int64_t n_src, int64_t d, sy_plan* p) {
       n_src);
 }
 
+// Token-count rule. With at most two tokens per CU the one-wave tiles leave
+// the CUs short of waves, and tiles that spread a token over four waves move
+// the same bytes sooner. Measured on MI355X, bf16 D = 2048 (forward and
+// forward + backward, us, plan tiles -> this rule):
+//   N=9  T=512: 9.41 -> 8.75,  25.0 -> 21.9     N=9  T=256: 8.95 -> 7.57, 23.7 -> 20.0
+//   N=4  T=512: 5.65 -> 5.07,  15.7 -> 14.1     N=16 T=512: 14.7 -> 13.6, 36.9 -> 32.7
+// At four tokens per CU (T = 1024) the one-wave tiles are faster again, and
+// N <= 2 gains nothing. Only 16-bit rows of four chunks a lane (W * VPL = 4)
+// were measured, so only those change. The forward takes (4,1) at up to one
+// token per CU, else (2,2); the backward (4,1).
+void apply_token_rule(int op, int64_t n_src, int64_t n_tok, sy_plan* p) {
+  if (op != SY_OP_FWD && op != SY_OP_BWD) return;
+  const bool tiled = p->family == SY_FAMILY_RESIDENT || p->family == SY_FAMILY_CHUNKED;
+  if (!tiled || n_src < 3 || n_src > 16 || p->elems_per_chunk != 8) return;
+  if (p->waves_per_token * p->chunks_per_lane != 4) return;
+  int cus = 0;
+  if (cu_count(&cus) != hipSuccess || cus < 1) return;
+  if (n_tok < 1 || n_tok > 2 * (int64_t)cus) return;
+  const int nr = n_src <= 4 ? 4 : n_src <= 9 ? 9 : 16;
+  const int w = op == SY_OP_BWD || n_tok <= cus ? 4 : 2;
+  if (!tile_listed(op, w, 4 / w, nr)) return;
+  set(p, SY_FAMILY_RESIDENT, w, 4 / w, nr, p->elems_per_chunk, op, n_src);
+}
+
+void apply_tile_rules(int op, int64_t n_src, int64_t n_tok, int64_t d, sy_plan* p) {
+  apply_token_rule(op, n_src, n_tok, p);
+  apply_tile_override(op, n_src, d, p);
+}
+
 }  // namespace sy

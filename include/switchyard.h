@@ -97,7 +97,11 @@ typedef struct sy_plan {
 /* Fill *out with the execution plan for op at the given shape. `aligned` says
  * whether every pointer and row start is 16-byte aligned (the vector paths need
  * it). SY_OP_BWD plans assume the forward's stats are passed (the operator's
- * path); a backward without stats may run a thinner tile. Replaces the dispatch helpers _launch_config, _bwd_launch and
+ * path); a backward without stats may run a thinner tile. The forward and
+ * backward launches also take the token count into account: with at most two
+ * tokens per CU (16-bit rows of four chunks a lane, 3 <= N <= 16) they run
+ * tiles of four or two waves per token, which sy_kernel_info reports and this
+ * function, having no token count, does not. Replaces the dispatch helpers _launch_config, _bwd_launch and
  * _batched_launch (src/switchyard/triton_op.py:130-150, :267-276, :420-435). */
 int sy_plan_for(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_dtype,
                 int aligned, sy_plan* out);
