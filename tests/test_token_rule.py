@@ -1,0 +1,63 @@
+"""The token-count tile rule (GPU): with at most two tokens per CU the forward
+runs (4,1,NR) up to one token per CU and (2,2,NR) up to two, the backward
+(4,1,NR); above that the plan's one-wave tiles. Each case checks, bit for bit,
+that the default launch equals the launch forced onto the expected tile with
+the SY_TILE_* measurement override, and that the result matches the float64
+oracle. Token counts are derived from the device's CU count.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+if not torch.cuda.is_available():  # pragma: no cover
+    pytest.skip("needs a HIP device", allow_module_level=True)
+
+from oracle import c_oracle  # noqa: E402
+from oracle.reference import dtype_floor, rel_l2  # noqa: E402
+from switchyard.hip_op import block_attn_res_hip  # noqa: E402
+
+DEV = "cuda"
+CUS = torch.cuda.get_device_properties(0).multi_processor_count
+
+
+def _run(n, t, d, seed):
+    g = torch.Generator().manual_seed(seed)
+    v = torch.randn(n, 1, t, d, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(d, generator=g) * 0.5).to(torch.bfloat16).to(DEV)
+    go = torch.randn(1, t, d, generator=g).to(torch.bfloat16).to(DEV)
+    vv, ww = v.clone().requires_grad_(), w.clone().requires_grad_()
+    out = block_attn_res_hip(vv, ww)
+    out.backward(go)
+    torch.cuda.synchronize()
+    return (v, w, go), (out.detach(), vv.grad, ww.grad)
+
+
+@pytest.mark.parametrize("n,per_cu,fwd_tile,bwd_tile", [
+    (9, 1, "4,1,9", "4,1,9"),
+    (9, 2, "2,2,9", "4,1,9"),
+    (4, 2, "2,2,4", "4,1,4"),
+    (16, 2, "2,2,16", "4,1,16"),
+    (9, 4, "1,4,9", "1,4,9"),
+])
+def test_default_launch_takes_the_rule_tile(monkeypatch, n, per_cu, fwd_tile, bwd_tile):
+    t, d = CUS * per_cu, 2048
+    print(f"token rule N={n} T={t} expect fwd {fwd_tile} bwd {bwd_tile}", flush=True)
+    monkeypatch.delenv("SY_TILE_FWD", raising=False)
+    monkeypatch.delenv("SY_TILE_BWD", raising=False)
+    ins, got = _run(n, t, d, seed=n + per_cu)
+    monkeypatch.setenv("SY_TILE_FWD", fwd_tile)
+    monkeypatch.setenv("SY_TILE_BWD", bwd_tile)
+    _, forced = _run(n, t, d, seed=n + per_cu)
+    for a, b, what in zip(got, forced, ("out", "dv", "dw")):
+        assert torch.equal(a, b), what
+    v, w, go = ins
+    ro = torch.as_tensor(c_oracle.forward(v[:, 0].double().cpu().numpy(), w.double().cpu().numpy()))
+    rdv, rdw = c_oracle.backward(v[:, 0].double().cpu().numpy(), w.double().cpu().numpy(),
+                                 go[0].double().cpu().numpy())
+    for x, ref, what in ((got[0][0].cpu(), ro, "out"), (got[1][:, 0].cpu(), torch.as_tensor(rdv), "dv"),
+                         (got[2].cpu(), torch.as_tensor(rdw), "dw")):
+        assert rel_l2(x, ref) <= 1.10 * dtype_floor(ref, torch.bfloat16), what
