@@ -892,10 +892,16 @@ hipError_t launch_mx(const BatchedArgs& a, hipStream_t s, KernelRes* info) {
 // until it catches up; two slots in step: 61.2 vs 72.8 us at config 3, 112.6 vs
 // 118.4 us at T = 8192. At smaller D or with 16 rows they are slower (D = 1024:
 // 39.2 vs 36.8 us; N=16 D=1536 S=16: 111.7 vs 85.0; N=5 D=512 S=6: 23.9 vs 19.3).
+// Nor below three tokens per CU, where two slots leave CUs idle (N=9, D=2048,
+// S=8: T=256 10.9 vs 9.0 us, T=512 11.7 vs 11.5; T=1024 equal, T=2048 33.2 vs
+// 36.1).
 template <class T, int KS, int NR, int SQ>
 hipError_t launch_mx_slots(const BatchedArgs& a, hipStream_t s, KernelRes* info) {
   const char* env = std::getenv("SY_MX_SLOTS");  // measurement knob: 1 or 2 slots
-  const int want = env != nullptr ? std::atoi(env) : (KS == 16 && NR <= 9 ? 2 : 1);
+  int cus = 0;
+  if (cu_count(&cus) != hipSuccess || cus < 1) cus = 1;
+  const bool enough = a.n_tok > 2 * (int64_t)cus;
+  const int want = env != nullptr ? std::atoi(env) : (KS == 16 && NR <= 9 && enough ? 2 : 1);
   KernelRes two;
   if (want == 2 && launch_mx<T, KS, NR, SQ, 2>(a, s, &two) == hipSuccess)
     return launch_mx<T, KS, NR, SQ, 2>(a, s, info);

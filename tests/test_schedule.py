@@ -266,11 +266,13 @@ def test_batched_matrix_kernel(nstd, dtype):
         _stat_close(ell[k, 0].cpu(), rl, f"l[{k}]")
 
 
-def test_batched_matrix_slots_agree(monkeypatch):
+@pytest.mark.parametrize("t", [777, 3])
+def test_batched_matrix_slots_agree(monkeypatch, t):
     """Two token slots per workgroup and one (the SY_MX_SLOTS measurement
     knob) give the same bits: the slots only change which workgroup computes
-    a token."""
-    v, _ = _make(9, 777, 2048, torch.bfloat16, seed=23)
+    a token. Three tokens forced onto two slots leave the second workgroup's
+    second slot empty."""
+    v, _ = _make(9, t, 2048, torch.bfloat16, seed=23)
     q = (torch.randn(8, 2048, generator=torch.Generator().manual_seed(24)) * 0.5).to(torch.bfloat16).to(DEV)
     outs = []
     for slots in ("2", "1"):
