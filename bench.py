@@ -471,8 +471,8 @@ def sweep_mode(args):
         fb_ms = harness.time_loop_median([lambda s=s: (fwd(s), bwd(s)) for s in sets], device=dev, iters=iters)
         fb = attn_res_train_bytes(n, b, t, d, item)
         fw = attn_res_min_bytes(n, b, t, d, item)
-        fplan = _lib.plan(_lib.OP_FWD, n, d, dt)
-        bplan = _lib.plan(_lib.OP_BWD, n, d, dt)
+        fplan = _lib.plan(_lib.OP_FWD, n, d, dt, n_tok=nt)
+        bplan = _lib.plan(_lib.OP_BWD, n, d, dt, n_tok=nt)
         rec = {"sweep": name, "impl": "switchyard_hip", "N": n, "B": b, "T": t, "D": d, "dtype": tag,
                "rotating_sets": rot,
                "fwd_us": round(f_ms * 1e3, 2), "fwd_gbps": round(fw / f_ms / 1e6, 1),

@@ -368,6 +368,16 @@ int sy_plan_for(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int 
   return make_plan(op, n_src, n_q, d, v_dtype, w_dtype, aligned, out);
 }
 
+int sy_plan_for_tokens(int op, int64_t n_src, int64_t n_q, int64_t n_tok, int64_t d, int v_dtype,
+                       int w_dtype, int aligned, sy_plan* out) {
+  if (out == nullptr) return SY_ERR_NULL;
+  if (n_tok < 0) return SY_ERR_SHAPE;
+  const int rc = make_plan(op, n_src, n_q, d, v_dtype, w_dtype, aligned, out);
+  if (rc != SY_OK) return rc;
+  if (op == SY_OP_FWD || op == SY_OP_BWD) apply_tile_rules(op, n_src, n_tok, d, out);
+  return SY_OK;
+}
+
 int sy_fwd(const void* v, const void* w, void* out, float* stats, int64_t n_src, int64_t n_tok,
            int64_t d, int64_t src_stride, int v_dtype, int w_dtype, float eps, void* stream) {
   // Empty tensors have NULL data pointers; with no tokens nothing is touched.

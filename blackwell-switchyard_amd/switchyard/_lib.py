@@ -56,6 +56,7 @@ class Plan(ctypes.Structure):
 SIGNATURES = {
     "sy_abi_version": (_i32, []),
     "sy_plan_for": (_i32, [_i32, _i64, _i64, _i64, _i32, _i32, _i32, ctypes.POINTER(Plan)]),
+    "sy_plan_for_tokens": (_i32, [_i32, _i64, _i64, _i64, _i64, _i32, _i32, _i32, ctypes.POINTER(Plan)]),
     "sy_fwd": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32, ctypes.c_float, _vp]),
     "sy_bwd_workspace_bytes": (_i64, [_i64, _i64, _i64, _i32, _i32]),
     "sy_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32, _i32,
@@ -131,11 +132,18 @@ def check(rc: int, what: str) -> None:
 
 
 def plan(op: int, n_src: int, d: int, dtype: torch.dtype, *, n_q: int = 0,
-         w_dtype: torch.dtype | None = None, aligned: bool = True) -> dict:
-    """The execution plan the library picks for a shape (pure host arithmetic)."""
+         w_dtype: torch.dtype | None = None, aligned: bool = True, n_tok: int | None = None) -> dict:
+    """The execution plan the library picks for a shape (pure host arithmetic).
+    With ``n_tok``, the tile a launch of that many tokens runs on the current
+    device (``sy_plan_for_tokens``: the forward and backward also depend on
+    the token count)."""
     p = Plan()
-    rc = lib().sy_plan_for(op, n_src, n_q, d, dtype_code(dtype), dtype_code(w_dtype or dtype),
-                           int(aligned), ctypes.byref(p))
+    if n_tok is None:
+        rc = lib().sy_plan_for(op, n_src, n_q, d, dtype_code(dtype), dtype_code(w_dtype or dtype),
+                               int(aligned), ctypes.byref(p))
+    else:
+        rc = lib().sy_plan_for_tokens(op, n_src, n_q, n_tok, d, dtype_code(dtype),
+                                      dtype_code(w_dtype or dtype), int(aligned), ctypes.byref(p))
     check(rc, "sy_plan_for")
     return p.as_dict()
 

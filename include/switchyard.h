@@ -106,6 +106,16 @@ typedef struct sy_plan {
 int sy_plan_for(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_dtype,
                 int aligned, sy_plan* out);
 
+/* sy_plan_for for a launch of n_tok tokens on the current device: for the
+ * forward and the backward, the tile sy_fwd / sy_bwd run, with the token-count
+ * rule and the SY_TILE_* measurement override applied; other ops as
+ * sy_plan_for. Without a device the token-count rule is skipped. No
+ * counterpart in the reference, whose launch configuration ignores the token
+ * count (src/switchyard/triton_op.py:130-150); it serves benchmarks and
+ * callers that report the launched tile. */
+int sy_plan_for_tokens(int op, int64_t n_src, int64_t n_q, int64_t n_tok, int64_t d, int v_dtype,
+                       int w_dtype, int aligned, sy_plan* out);
+
 /* Forward of the autograd operator: out = AttnRes(v, w).
  * Replaces _BlockAttnResTriton.forward and its _fwd_resident/_fwd_tiled
  * launches (src/switchyard/triton_op.py:505-536, :50-117).

@@ -314,3 +314,17 @@ def test_planner_rejects_bad_input():
     assert lib.sy_plan_for(0, 9, 0, 2048, 3, BF16, 1, ctypes.byref(p)) == DTYPE
     assert lib.sy_plan_for(0, 9, 0, 2048, BF16, BF16, 1, None) == NULL
     assert lib.sy_plan_for(0, 5000, 0, 7, BF16, BF16, 1, ctypes.byref(p)) == SHAPE
+
+
+def test_plan_for_tokens_checks_input_and_matches_the_plan_without_a_device():
+    """Without a device the token-count rule is skipped, so the plan for a
+    launch equals sy_plan_for; bad arguments are rejected the same way."""
+    lib = _lib.lib()
+    p, q = _lib.Plan(), _lib.Plan()
+    assert lib.sy_plan_for_tokens(0, 9, 0, 512, 2048, BF16, BF16, 1, None) == NULL
+    assert lib.sy_plan_for_tokens(0, 9, 0, -1, 2048, BF16, BF16, 1, ctypes.byref(p)) == SHAPE
+    assert lib.sy_plan_for_tokens(9, 9, 0, 512, 2048, BF16, BF16, 1, ctypes.byref(p)) == OP
+    for op in (0, 1, 3):
+        assert lib.sy_plan_for_tokens(op, 9, 0, 512, 2048, BF16, BF16, 1, ctypes.byref(p)) == OK
+        assert lib.sy_plan_for(op, 9, 0, 2048, BF16, BF16, 1, ctypes.byref(q)) == OK
+        assert p.as_dict() == q.as_dict()

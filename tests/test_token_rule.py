@@ -61,3 +61,15 @@ def test_default_launch_takes_the_rule_tile(monkeypatch, n, per_cu, fwd_tile, bw
     for x, ref, what in ((got[0][0].cpu(), ro, "out"), (got[1][:, 0].cpu(), torch.as_tensor(rdv), "dv"),
                          (got[2].cpu(), torch.as_tensor(rdw), "dw")):
         assert rel_l2(x, ref) <= 1.10 * dtype_floor(ref, torch.bfloat16), what
+
+
+@pytest.mark.parametrize("per_cu,fwd_tile,bwd_tile", [(1, (4, 1, 9), (4, 1, 9)), (2, (2, 2, 9), (4, 1, 9)),
+                                                      (16, (1, 4, 9), (1, 4, 9))])
+def test_plan_for_tokens_reports_the_launched_tile(monkeypatch, per_cu, fwd_tile, bwd_tile):
+    from switchyard import _lib
+
+    monkeypatch.delenv("SY_TILE_FWD", raising=False)
+    monkeypatch.delenv("SY_TILE_BWD", raising=False)
+    for op, want in ((_lib.OP_FWD, fwd_tile), (_lib.OP_BWD, bwd_tile)):
+        p = _lib.plan(op, 9, 2048, torch.bfloat16, n_tok=CUS * per_cu)
+        assert (p["waves_per_token"], p["chunks_per_lane"], p["rows_per_tile"]) == want
