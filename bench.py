@@ -740,8 +740,10 @@ def main() -> None:
         return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus > 1 or world > 1:
-        print("bench.py: this build measures one GPU only (the operator is independent per token; "
-              "see DESIGN.md for how it shards). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py: this build measures one GPU only. Tokens are independent, so the operator "
+              "shards over B*T with no communication in the forward and one 4*D-byte all-reduce of "
+              "dw in the backward; one GPU's share is the number measured here. Run with --gpus 1.",
+              file=sys.stderr)
         sys.exit(2)
     if args.summarize is not None:
         summarize(args)
