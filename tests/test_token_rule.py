@@ -24,11 +24,11 @@ DEV = "cuda"
 CUS = torch.cuda.get_device_properties(0).multi_processor_count
 
 
-def _run(n, t, d, seed):
+def _run(n, t, d, seed, dtype=torch.bfloat16):
     g = torch.Generator().manual_seed(seed)
-    v = torch.randn(n, 1, t, d, generator=g).to(torch.bfloat16).to(DEV)
-    w = (torch.randn(d, generator=g) * 0.5).to(torch.bfloat16).to(DEV)
-    go = torch.randn(1, t, d, generator=g).to(torch.bfloat16).to(DEV)
+    v = torch.randn(n, 1, t, d, generator=g).to(dtype).to(DEV)
+    w = (torch.randn(d, generator=g) * 0.5).to(dtype).to(DEV)
+    go = torch.randn(1, t, d, generator=g).to(dtype).to(DEV)
     vv, ww = v.clone().requires_grad_(), w.clone().requires_grad_()
     out = block_attn_res_hip(vv, ww)
     out.backward(go)
@@ -36,22 +36,23 @@ def _run(n, t, d, seed):
     return (v, w, go), (out.detach(), vv.grad, ww.grad)
 
 
-@pytest.mark.parametrize("n,per_cu,fwd_tile,bwd_tile", [
-    (9, 1, "4,1,9", "4,1,9"),
-    (9, 2, "2,2,9", "4,1,9"),
-    (4, 2, "2,2,4", "4,1,4"),
-    (16, 2, "2,2,16", "4,1,16"),
-    (9, 4, "1,4,9", "1,4,9"),
+@pytest.mark.parametrize("n,per_cu,fwd_tile,bwd_tile,dtype", [
+    (9, 1, "4,1,9", "4,1,9", torch.bfloat16),
+    (9, 2, "2,2,9", "4,1,9", torch.bfloat16),
+    (9, 2, "2,2,9", "4,1,9", torch.float16),
+    (4, 2, "2,2,4", "4,1,4", torch.bfloat16),
+    (16, 2, "2,2,16", "4,1,16", torch.bfloat16),
+    (9, 4, "1,4,9", "1,4,9", torch.bfloat16),
 ])
-def test_default_launch_takes_the_rule_tile(monkeypatch, n, per_cu, fwd_tile, bwd_tile):
+def test_default_launch_takes_the_rule_tile(monkeypatch, n, per_cu, fwd_tile, bwd_tile, dtype):
     t, d = CUS * per_cu, 2048
-    print(f"token rule N={n} T={t} expect fwd {fwd_tile} bwd {bwd_tile}", flush=True)
+    print(f"token rule N={n} T={t} {dtype} expect fwd {fwd_tile} bwd {bwd_tile}", flush=True)
     monkeypatch.delenv("SY_TILE_FWD", raising=False)
     monkeypatch.delenv("SY_TILE_BWD", raising=False)
-    ins, got = _run(n, t, d, seed=n + per_cu)
+    ins, got = _run(n, t, d, seed=n + per_cu, dtype=dtype)
     monkeypatch.setenv("SY_TILE_FWD", fwd_tile)
     monkeypatch.setenv("SY_TILE_BWD", bwd_tile)
-    _, forced = _run(n, t, d, seed=n + per_cu)
+    _, forced = _run(n, t, d, seed=n + per_cu, dtype=dtype)
     for a, b, what in zip(got, forced, ("out", "dv", "dw")):
         assert torch.equal(a, b), what
     v, w, go = ins
@@ -60,7 +61,7 @@ def test_default_launch_takes_the_rule_tile(monkeypatch, n, per_cu, fwd_tile, bw
                                  go[0].double().cpu().numpy())
     for x, ref, what in ((got[0][0].cpu(), ro, "out"), (got[1][:, 0].cpu(), torch.as_tensor(rdv), "dv"),
                          (got[2].cpu(), torch.as_tensor(rdw), "dw")):
-        assert rel_l2(x, ref) <= 1.10 * dtype_floor(ref, torch.bfloat16), what
+        assert rel_l2(x, ref) <= 1.10 * dtype_floor(ref, dtype), what
 
 
 @pytest.mark.parametrize("per_cu,fwd_tile,bwd_tile", [(1, (4, 1, 9), (4, 1, 9)), (2, (2, 2, 9), (4, 1, 9)),
