@@ -2,7 +2,7 @@
 // Every check that can be made on the host is made before any device work,
 // so bad arguments come back as negative sy_status codes. Nothing here
 // allocates device memory.
-#include <cstdlib>
+#include <atomic>
 #include <map>
 #include <mutex>
 
@@ -27,6 +27,12 @@ int status(hipError_t e) { return e == hipSuccess ? SY_OK : (int)e; }
 std::mutex g_mu;
 std::map<int, int> g_cus;                                   // device -> CU count
 
+// Measurement overrides (sy_tuning_set). g_tuning_on is read on every launch
+// without the lock; the struct itself only under it.
+std::mutex g_tuning_mu;
+std::atomic<bool> g_tuning_on{false};
+sy_tuning g_tuning{};
+
 // variant: 0 operator over stacked rows, 1 over per-row pointers, 2 the
 // (o, m, l) gradient over stacked rows (BwdVariant in sy_kernels.hpp).
 hipError_t bwd_resources(const sy_plan& p, int dtype, bool stats, int variant, KernelRes* out) {
@@ -50,11 +56,9 @@ int bwd_grid(const sy_plan& p, int64_t n_tok, int dtype, bool stats, int variant
     if (e != hipSuccess) return (int)e;
     per_cu = r.blocks_per_cu;
   }
-  // Tuning knob for measurement sweeps: workgroups per CU of the persistent grid.
-  if (const char* env = std::getenv("SY_BWD_BLOCKS_PER_CU")) {
-    const int k = std::atoi(env);
-    if (k >= 1 && k <= 64) per_cu = k;
-  }
+  // Measurement override (sy_tuning_set): workgroups per CU of the persistent grid.
+  sy_tuning t;
+  if (tuning_snapshot(&t) && t.bwd_blocks_per_cu > 0) per_cu = t.bwd_blocks_per_cu;
   const int64_t slots = (n_tok + p.tokens_per_block - 1) / p.tokens_per_block;
   int64_t g = (int64_t)cus * per_cu;
   if (g > slots) g = slots;
@@ -224,6 +228,14 @@ int listed_rows(const void* const* rows, int64_t n_src, RowTable* t, bool* rows_
 }
 
 }  // namespace
+
+bool tuning_snapshot(sy_tuning* out) {
+  if (!g_tuning_on.load(std::memory_order_acquire)) return false;
+  std::lock_guard<std::mutex> lk(g_tuning_mu);
+  if (!g_tuning_on.load(std::memory_order_relaxed)) return false;
+  *out = g_tuning;
+  return true;
+}
 
 hipError_t cu_count(int* out) {
   int dev = 0;
@@ -721,6 +733,32 @@ int sy_bw_probe(int kind, const void* src, void* dst, int64_t bytes, void* strea
   if ((kind != 1 && src == nullptr) || dst == nullptr) return SY_ERR_NULL;
   if ((kind != 1 && !al16(src)) || (kind != 0 && !al16(dst))) return SY_ERR_SHAPE;
   return status(launch_probe(kind, src, dst, bytes, (int)sy_probe_grid(bytes), (hipStream_t)stream));
+}
+
+int sy_tuning_set(const sy_tuning* t) {
+  if (t != nullptr) {
+    for (const int32_t* f : {t->fwd_tile, t->bwd_tile, t->batched_tile, t->sol_tile})
+      for (int k = 0; k < 3; ++k)
+        if (f[k] < 0 || f[k] > 64) return SY_ERR_SHAPE;
+    if (t->bwd_blocks_per_cu < 0 || t->bwd_blocks_per_cu > 64) return SY_ERR_SHAPE;
+    if (t->mx_slots < 0 || t->mx_slots > 2) return SY_ERR_SHAPE;
+    if (t->bmx_waves != 0 && t->bmx_waves != 4) return SY_ERR_SHAPE;
+  }
+  std::lock_guard<std::mutex> lk(g_tuning_mu);
+  if (t == nullptr) {
+    g_tuning = sy_tuning{};
+    g_tuning_on.store(false, std::memory_order_release);
+  } else {
+    g_tuning = *t;
+    g_tuning_on.store(true, std::memory_order_release);
+  }
+  return SY_OK;
+}
+
+int sy_tuning_get(sy_tuning* out) {
+  if (out == nullptr) return SY_ERR_NULL;
+  if (!tuning_snapshot(out)) *out = sy_tuning{};
+  return SY_OK;
 }
 
 const char* sy_strerror(int code) {

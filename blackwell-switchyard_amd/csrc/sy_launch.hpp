@@ -174,13 +174,19 @@ struct BwdBatchedArgs {
 int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_dtype, int aligned,
               sy_plan* out, int has_stats = 1, int matrix_ok = 1);
 
-// Launch-time tile override from the SY_TILE_* environment variables
-// (sy_plan.cpp); sy_plan_for never applies it.
+// Measurement overrides installed with sy_tuning_set (sy_capi.cpp). Returns
+// false (and leaves *out untouched) when none are installed, which is the
+// default: then no launch depends on anything but shape, dtype, alignment
+// and device.
+bool tuning_snapshot(sy_tuning* out);
+
+// Launch-time tile override from sy_tuning_set (sy_plan.cpp); sy_plan_for
+// never applies it.
 void apply_tile_override(int op, int64_t n_src, int64_t d, sy_plan* p);
 // The plan's tile for n_tok tokens: the token-count rule (wider tiles when
-// there are at most two tokens per CU, forward and backward), then the
-// SY_TILE_* measurement override. Every launch and size query of the forward
-// and backward applies it, so grids and workspaces agree.
+// there are at most two tokens per CU, forward and backward), then any
+// sy_tuning_set tile override. Every launch and size query of the forward and
+// backward applies it, so grids and workspaces agree.
 void apply_tile_rules(int op, int64_t n_src, int64_t n_tok, int64_t d, sy_plan* p);
 
 // Launches the matrix-core batched forward (a.n_src etc. must pass

@@ -897,11 +897,12 @@ hipError_t launch_mx(const BatchedArgs& a, hipStream_t s, KernelRes* info) {
 // 36.1).
 template <class T, int KS, int NR, int SQ>
 hipError_t launch_mx_slots(const BatchedArgs& a, hipStream_t s, KernelRes* info) {
-  const char* env = std::getenv("SY_MX_SLOTS");  // measurement knob: 1 or 2 slots
   int cus = 0;
   if (cu_count(&cus) != hipSuccess || cus < 1) cus = 1;
   const bool enough = a.n_tok > 2 * (int64_t)cus;
-  const int want = env != nullptr ? std::atoi(env) : (KS == 16 && NR <= 9 && enough ? 2 : 1);
+  int want = KS == 16 && NR <= 9 && enough ? 2 : 1;
+  sy_tuning t;  // measurement override: 1 or 2 slots
+  if (tuning_snapshot(&t) && t.mx_slots > 0) want = t.mx_slots;
   KernelRes two;
   if (want == 2 && launch_mx<T, KS, NR, SQ, 2>(a, s, &two) == hipSuccess)
     return launch_mx<T, KS, NR, SQ, 2>(a, s, info);
@@ -977,8 +978,9 @@ hipError_t launch_bmx_rows(const BwdBatchedArgs& a, int grid, hipStream_t s, Ker
 template <class T>
 hipError_t launch_bmx_dtype(const BwdBatchedArgs& a, int grid, hipStream_t s, KernelRes* info) {
   int w = bwd_matrix_waves(a.d);
-  // Measurement knob: four waves per workgroup where that tile exists.
-  if (const char* env = std::getenv("SY_BMX_WAVES")) w = std::atoi(env) == 4 ? 4 : w;
+  // Measurement override: four waves per workgroup where that tile exists.
+  sy_tuning t;
+  if (tuning_snapshot(&t) && t.bmx_waves == 4) w = 4;
   if (w == 8) {
     switch (a.d) {
       case 1024: return launch_bmx_rows<T, 4, 8>(a, grid, s, info);

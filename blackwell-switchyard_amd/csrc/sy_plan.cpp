@@ -32,9 +32,6 @@
 //     do not fit; otherwise one chunk per lane on the fewest waves that cover the row,
 //     N <= 9 and S <= 8 (dv and dq accumulators stay in registers); otherwise
 //     the generic kernel while its LDS scalars fit.
-#include <cstdio>
-#include <cstdlib>
-
 #include "../../include/switchyard.h"
 #include "sy_launch.hpp"
 
@@ -223,21 +220,20 @@ bool tile_listed(int op, int w, int vpl, int nr) {
   return false;
 }
 
-// Tuning knob for measurement sweeps: SY_TILE_FWD / SY_TILE_BWD /
-// SY_TILE_BATCHED / SY_TILE_SOL = "W,VPL,NR" replaces the tile of a vector
-// plan when that tile is built, covers the row, and (backward, batched) holds
-// every row. Anything else leaves the plan untouched.
+// Measurement override (sy_tuning_set): a forced "W,VPL,NR" tile replaces the
+// tile of a vector plan when that tile is built, covers the row, and
+// (backward, batched) holds every row. Anything else leaves the plan untouched.
 void apply_tile_override(int op, int64_t n_src, int64_t d, sy_plan* p) {
   const bool tiled = p->family == SY_FAMILY_RESIDENT || p->family == SY_FAMILY_CHUNKED;
   if (!tiled && !(op == SY_OP_BATCHED && p->family == SY_FAMILY_MATRIX)) return;
-  const char* name = op == SY_OP_FWD ? "SY_TILE_FWD"
-                     : op == SY_OP_BWD ? "SY_TILE_BWD"
-                     : op == SY_OP_BATCHED ? "SY_TILE_BATCHED"
-                                           : "SY_TILE_SOL";
-  const char* s = std::getenv(name);
-  int w = 0, vpl = 0, nr = 0;
-  if (s == nullptr || std::sscanf(s, "%d,%d,%d", &w, &vpl, &nr) != 3) return;
-  if (!tile_listed(op, w, vpl, nr)) return;
+  sy_tuning t;
+  if (!tuning_snapshot(&t)) return;
+  const int32_t* f = op == SY_OP_FWD ? t.fwd_tile
+                     : op == SY_OP_BWD ? t.bwd_tile
+                     : op == SY_OP_BATCHED ? t.batched_tile
+                                           : t.sol_tile;
+  const int w = f[0], vpl = f[1], nr = f[2];
+  if (w == 0 || !tile_listed(op, w, vpl, nr)) return;
   if ((int64_t)64 * w * vpl < d / p->elems_per_chunk) return;
   const bool can_chunk = op == SY_OP_FWD || op == SY_OP_SOL;
   if (nr < n_src && !can_chunk) return;

@@ -9,6 +9,7 @@ missing every operator raises.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import pathlib
 import threading
@@ -52,6 +53,20 @@ class Plan(ctypes.Structure):
         return d
 
 
+class Tuning(ctypes.Structure):
+    """Mirror of ``sy_tuning`` (measurement-only launch overrides)."""
+
+    _fields_ = [
+        ("fwd_tile", ctypes.c_int32 * 3),
+        ("bwd_tile", ctypes.c_int32 * 3),
+        ("batched_tile", ctypes.c_int32 * 3),
+        ("sol_tile", ctypes.c_int32 * 3),
+        ("bwd_blocks_per_cu", ctypes.c_int32),
+        ("mx_slots", ctypes.c_int32),
+        ("bmx_waves", ctypes.c_int32),
+    ]
+
+
 #: Every symbol include/switchyard.h declares, with (restype, argtypes).
 SIGNATURES = {
     "sy_abi_version": (_i32, []),
@@ -86,6 +101,8 @@ SIGNATURES = {
                               ctypes.c_float, _vp]),
     "sy_bw_probe": (_i32, [_i32, _vp, _vp, _i64, _vp]),
     "sy_probe_grid": (_i64, [_i64]),
+    "sy_tuning_set": (_i32, [ctypes.POINTER(Tuning)]),
+    "sy_tuning_get": (_i32, [ctypes.POINTER(Tuning)]),
     "sy_strerror": (ctypes.c_char_p, [_i32]),
 }
 
@@ -156,3 +173,34 @@ def pointer_table(tensors) -> ctypes.Array:
 def stream_ptr(device: torch.device) -> ctypes.c_void_p:
     """The HIP stream torch is currently issuing work on for ``device``."""
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+@contextlib.contextmanager
+def tuning(**overrides):
+    """Install measurement-only launch overrides (``sy_tuning_set``) for the
+    duration of a ``with`` block, then restore what was installed before.
+
+    Keys: ``fwd_tile``, ``bwd_tile``, ``batched_tile``, ``sol_tile`` as
+    ``(W, VPL, NR)`` tuples; ``bwd_blocks_per_cu``, ``mx_slots``,
+    ``bmx_waves`` as ints. Only sweeps and tile-forcing tests use this; the
+    library's default launches read nothing but their arguments.
+    """
+    so = lib()
+    before = Tuning()
+    check(so.sy_tuning_get(ctypes.byref(before)), "sy_tuning_get")
+    t = Tuning()
+    ctypes.memmove(ctypes.byref(t), ctypes.byref(before), ctypes.sizeof(Tuning))
+    for key, val in overrides.items():
+        if key.endswith("_tile"):
+            getattr(t, key)[:] = [int(x) for x in val]
+        else:
+            setattr(t, key, int(val))
+    check(so.sy_tuning_set(ctypes.byref(t)), "sy_tuning_set")
+    try:
+        yield
+    finally:
+        if any(getattr(before, f)[k] if f.endswith("_tile") else getattr(before, f)
+               for f, _ in Tuning._fields_ for k in (range(3) if f.endswith("_tile") else [0])):
+            so.sy_tuning_set(ctypes.byref(before))
+        else:
+            so.sy_tuning_set(None)

@@ -240,6 +240,53 @@ def environment() -> dict:
     }
 
 
+#: Files whose content identifies a build of this repository.
+_SOURCE_GLOBS = ("blackwell-switchyard_amd/csrc/*.cpp", "blackwell-switchyard_amd/csrc/*.hip",
+                 "blackwell-switchyard_amd/csrc/*.hpp", "blackwell-switchyard_amd/csrc/Makefile",
+                 "blackwell-switchyard_amd/switchyard/*.py", "include/*.h", "bench.py",
+                 "__graft_entry__.py")
+BUILD_INFO = "blackwell-switchyard_amd/switchyard/_build_info.json"
+
+
+def source_fingerprint(root) -> str:
+    """SHA-256 over the sources that make the library and the bench (sorted
+    relative paths and contents): identifies the code a number came from on
+    a machine where no git history exists."""
+    import hashlib
+    import pathlib
+
+    root = pathlib.Path(root)
+    h = hashlib.sha256()
+    for pattern in _SOURCE_GLOBS:
+        for f in sorted(root.glob(pattern)):
+            h.update(str(f.relative_to(root)).encode())
+            h.update(b"\0")
+            h.update(f.read_bytes())
+    return h.hexdigest()
+
+
+def provenance(root, *, argv, seeds) -> dict:
+    """What produced a record (reference bench/harness.py:42-70): the git
+    commit and dirty flag recorded when the library was built (the GPU box
+    carries no git history), the source fingerprint then and now, argv and
+    seeds."""
+    import json
+    import pathlib
+
+    root = pathlib.Path(root)
+    live = source_fingerprint(root)
+    info = {}
+    try:
+        info = json.loads((root / BUILD_INFO).read_text())
+    except (OSError, ValueError):
+        pass
+    commit = repository_commit(str(root)) or info.get("commit")
+    return {"commit": commit, "dirty_at_build": info.get("dirty"), "built_at": info.get("built_at"),
+            "build_fingerprint": info.get("fingerprint"), "source_fingerprint": live,
+            "sources_match_build": info.get("fingerprint") == live if info else None,
+            "argv": list(argv), "seeds": seeds}
+
+
 def repository_commit(path: str) -> str | None:
     try:
         r = subprocess.run(["git", "-C", path, "rev-parse", "HEAD"], capture_output=True, text=True,

@@ -1,41 +1,61 @@
-"""Decoder-only Transformer with a switchable residual mechanism.
+"""Decoder-only Transformer whose residual stream can be Block AttnRes.
 
-Restates the reference's ``switchyard.model`` (src/switchyard/model.py of
-sabdulmajid/blackwell-switchyard): the same three residual modes, the same
-Block AttnRes wiring (paper Eq. 6, two sites per layer plus a readout site),
-and the same source arena, with the ``"switchyard"`` mode calling the HIP
-operator.
+This is the operator's training caller (the reference's ``switchyard.model``,
+src/switchyard/model.py of sabdulmajid/blackwell-switchyard): the same public
+names (``ModelConfig``, ``Transformer``, ``source_count_schedule``,
+``slab_copies``), the same three residual mechanisms and the same wiring of
+the paper's Eq. 6, so that the step-time comparison between mechanisms means
+the same thing here.
 
-Residual modes (model.py:132-143):
-  ``standard``    PreNorm ``x = x + sublayer(norm(x))`` -- the control.
-  ``attnres``     Block AttnRes through the eager ``folded_form``.
-  ``switchyard``  Block AttnRes through the HIP operator.
+Residual mechanisms (``ModelConfig.residual``):
+  ``standard``    PreNorm, ``x <- x + f(norm(x))``: the control.
+  ``attnres``     Block AttnRes evaluated by the eager ``folded_form``.
+  ``switchyard``  Block AttnRes evaluated by the HIP operator.
 
-Block AttnRes wiring (model.py:26-57). A sublayer is the paper's "layer"; the
-``2 * n_layers`` sublayers are split into ``n_blocks`` blocks. ``blocks[0]`` is
-the embedding, ``blocks[j]`` the completed block ``j``; ``partial`` is the
-unweighted running sum of the current block's sublayer outputs. Sublayer ``i``
-attends over ``blocks[0..n]`` (plus ``partial`` unless it opens its block);
-its output replaces the residual stream input. A readout site over every block
-feeds the LM head.
+Wiring. A "layer" of the paper is a sublayer here (attention or MLP, each
+behind its own RMSNorm), and the ``2 * n_layers`` sublayers are cut into
+``n_blocks`` equal blocks. The stream keeps the completed block
+representations (the embedding first) and the running, unweighted sum of the
+current block's sublayer outputs. Each sublayer reads ``AttnRes`` over the
+completed blocks plus the running sum (absent for the first sublayer of a
+block) and adds its output to the running sum; when a block ends, its running
+sum becomes its representation. A final site over every completed block feeds
+the LM head. Each site owns a pseudo-query and an RMSNorm gain, both of width
+``d_model`` (2 * d_model parameters a site).
 
-Source arena (model.py:59-104). Instead of ``torch.stack`` at every site, one
-``[n_blocks + 1, B, T, D]`` buffer holds the embedding in slot 0, block ``j``
-in slot ``j`` and the running partial in the next free slot (whose final value
-*is* the next block, so a block boundary writes nothing). Each site hands the
-operator ``arena[:n_src]`` -- a contiguous prefix, which the HIP op reads in
-place through its source stride. The prefix is an alias made with
-``Tensor.set_`` so it has its own autograd version counter; the partial slot,
-the only slot rewritten later, is restored from the saved partial before the
-site's backward runs. Sites' backwards run in reverse order, so each restore
-happens after every later site is done with the slot.
+How a site's sources reach the operator (``ModelConfig.sources``):
+  ``stack``  ``torch.stack`` of the live tensors at every site: N slab copies
+             per site (the paper's pseudocode).
+  ``arena``  one ``[n_blocks + 1, B, T, D]`` buffer per forward. The
+             embedding is copied into slot 0 and each new running sum into the
+             slot of the block being built, so a site's sources are always the
+             buffer's first N slots, read in place: one slab copy per sublayer.
+  ``table``  (HIP operator only) the site passes the live tensors' addresses
+             to the pointer-table entry points; nothing is copied. At most 16
+             sources per site (the table size); wider sites stack.
+
+Autograd over the arena. The running-sum slot is overwritten by every later
+sublayer of its block while earlier sites still need, for their backward, the
+value they read. Two mechanisms handle that:
+  * HIP sites call the C ABI themselves. The forward reads the buffer prefix
+    through its source stride; the backward addresses the completed-block
+    slots in the buffer (each written once, when its block ended, and never
+    again) and the site's running sum through the tensor itself, with the
+    pointer-table backward -- so no slot is ever restored or copied back.
+  * Eager sites hand ``folded_form`` a view of the prefix. Every tensor that
+    autograd saves out of the buffer passes through a saved-tensor hook whose
+    unpack puts the site's running sum back into its slot before handing the
+    view over. The backward of a site runs only after every later site that
+    reads the slot has finished its own (each later site depends on this
+    site's output through the running sum), so the restored value is never
+    needed elsewhere. Saved-tensor hooks also bypass autograd's storage-wide
+    version check, which the slot writes would otherwise trip.
 """
 
 from __future__ import annotations
 
 import contextlib
 import math
-from collections.abc import Callable
 from dataclasses import dataclass
 
 import torch
@@ -56,27 +76,20 @@ __all__ = [
 ]
 
 RESIDUAL_MODES = ("standard", "attnres", "switchyard")
-SOURCE_MODES = ("arena", "stack")
+SOURCE_MODES = ("arena", "stack", "table")
 
 
-def _hip_impl(v: Tensor, w: Tensor, eps: float) -> Tensor:
-    from .hip_op import block_attn_res_hip
-
-    return block_attn_res_hip(v, w, eps)
-
-
-#: Residual mode -> operator ``(v, w, eps) -> [B, T, D]``.
-_IMPLS: dict[str, Callable[[Tensor, Tensor, float], Tensor]] = {
-    "attnres": folded_form,
-    "switchyard": _hip_impl,
-}
+# --------------------------------------------------------------------------
+# Configuration and the Eq. 6 bookkeeping
+# --------------------------------------------------------------------------
 
 
 @dataclass
 class ModelConfig:
-    """Model shape (model.py:151-202). Defaults: the 1.3B configuration of
-    BASELINE.json (24 layers, d_model 2048, 16 heads, 8 blocks, vocab 32000;
-    the reference used 32768)."""
+    """Model shape and residual mechanism (field names and meaning as the
+    reference's ``ModelConfig``, model.py:151-202). Defaults: the 1.3B
+    benchmark decoder -- 24 layers, d_model 2048, 16 heads, d_ff 5632, 8
+    blocks, vocab 32000 (the reference used 32768)."""
 
     vocab_size: int = 32000
     d_model: int = 2048
@@ -92,20 +105,25 @@ class ModelConfig:
     sources: str = "arena"
 
     def __post_init__(self) -> None:
+        problems = []
         if self.residual not in RESIDUAL_MODES:
-            raise ValueError(f"residual must be one of {RESIDUAL_MODES}, got {self.residual!r}")
+            problems.append(f"residual must be one of {RESIDUAL_MODES}, got {self.residual!r}")
         if self.sources not in SOURCE_MODES:
-            raise ValueError(f"sources must be one of {SOURCE_MODES}, got {self.sources!r}")
-        if self.d_model % self.n_heads:
-            raise ValueError(f"d_model {self.d_model} not divisible by n_heads {self.n_heads}")
-        if self.n_sublayers % self.n_blocks:
-            raise ValueError(
-                f"n_blocks {self.n_blocks} must divide the sublayer count {self.n_sublayers} "
-                "(= 2 * n_layers); a block is a whole number of sublayers"
-            )
+            problems.append(f"sources must be one of {SOURCE_MODES}, got {self.sources!r}")
+        elif self.sources == "table" and self.residual == "attnres":
+            problems.append("sources='table' passes device pointers to the HIP operator; "
+                            "the eager 'attnres' mechanism needs 'arena' or 'stack'")
+        if self.d_model % self.n_heads != 0:
+            problems.append(f"d_model {self.d_model} is not a multiple of n_heads {self.n_heads}")
+        if (2 * self.n_layers) % self.n_blocks != 0:
+            problems.append(f"n_blocks {self.n_blocks} does not divide the {2 * self.n_layers} "
+                            "sublayers (2 * n_layers) into whole blocks")
+        if problems:
+            raise ValueError("; ".join(problems))
 
     @property
     def n_sublayers(self) -> int:
+        """Attention and MLP of every layer: the paper's "layers"."""
         return 2 * self.n_layers
 
     @property
@@ -118,143 +136,275 @@ class ModelConfig:
 
     @property
     def uses_attnres(self) -> bool:
-        return self.residual != "standard"
+        return self.residual in ("attnres", "switchyard")
 
 
 def source_count_schedule(n_sublayers: int, n_blocks: int) -> list[int]:
-    """Sources each AttnRes site attends over (paper Eq. 6, model.py:205-219):
-    sublayer ``i`` of block ``k = i // block_size`` sees ``k + 1`` blocks, plus
-    the partial unless it opens its block; the last entry is the readout."""
-    per_block = n_sublayers // n_blocks
-    counts = []
-    for i in range(n_sublayers):
-        k, opens = divmod(i, per_block)
-        counts.append(k + 1 + (0 if opens == 0 else 1))
+    """Source count of every AttnRes site in order (paper Eq. 6; the reference
+    states it at model.py:205-219): in block ``j`` the opening sublayer sees
+    the embedding and the ``j`` completed blocks, every other sublayer also the
+    running sum; the readout site sees all ``n_blocks + 1`` representations."""
+    size = n_sublayers // n_blocks
+    counts: list[int] = []
+    for j in range(n_blocks):
+        counts += [j + 1] + [j + 2] * (size - 1)
     return counts + [n_blocks + 1]
 
 
 def slab_copies(n_sublayers: int, n_blocks: int, sources: str) -> int:
-    """``B*T*D`` slabs copied to stage sources in one forward (model.py:222-235):
-    stacking copies every source at every site; the arena writes the embedding
-    once and the partial once per sublayer."""
+    """``B*T*D`` slabs copied to present the sources over one forward
+    (model.py:222-235): ``stack`` copies every source at every site, ``arena``
+    the embedding once plus one running sum per sublayer, ``table`` nothing."""
     if sources == "stack":
         return sum(source_count_schedule(n_sublayers, n_blocks))
-    return n_sublayers + 1
+    if sources == "arena":
+        return n_sublayers + 1
+    if sources == "table":
+        return 0
+    raise ValueError(f"unknown source mode {sources!r}")
 
 
 # --------------------------------------------------------------------------
-# Standard decoder pieces (identical in every mode)
+# Decoder blocks (the same in every residual mode)
 # --------------------------------------------------------------------------
 
 
 class RMSNorm(nn.Module):
+    """``x / rms(x) * weight``, the statistic in fp32."""
+
     def __init__(self, d: int, eps: float) -> None:
         super().__init__()
         self.eps = eps
         self.weight = nn.Parameter(torch.ones(d))
 
     def forward(self, x: Tensor) -> Tensor:
-        scale = torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + self.eps).to(x.dtype)
-        return x * scale * self.weight
+        inv = x.float().square().mean(dim=-1, keepdim=True).add(self.eps).rsqrt()
+        return x * inv.to(x.dtype) * self.weight
 
 
-def _rope_tables(max_len: int, head_dim: int, theta: float) -> tuple[Tensor, Tensor]:
-    freqs = theta ** (-torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim)
-    ang = torch.arange(max_len, dtype=torch.float32)[:, None] * freqs[None, :]
-    return ang.cos(), ang.sin()
+class Rotary(nn.Module):
+    """Rotary position embedding on ``[B, T, H, hd]``: channel ``i`` of the
+    first half turns with channel ``i`` of the second half by ``t * theta^(-2i/hd)``."""
+
+    def __init__(self, head_dim: int, max_len: int, theta: float) -> None:
+        super().__init__()
+        half = head_dim // 2
+        inv_freq = torch.pow(theta, -torch.arange(half, dtype=torch.float32) * 2.0 / head_dim)
+        phase = torch.arange(max_len, dtype=torch.float32)[:, None] * inv_freq[None, :]
+        self.register_buffer("cos", phase.cos()[:, None, :], persistent=False)  # [T, 1, half]
+        self.register_buffer("sin", phase.sin()[:, None, :], persistent=False)
+
+    def forward(self, x: Tensor) -> Tensor:
+        t = x.shape[1]
+        c, s = self.cos[:t], self.sin[:t]
+        lo, hi = x.float().chunk(2, dim=-1)
+        return torch.cat((lo * c - hi * s, lo * s + hi * c), dim=-1).to(x.dtype)
 
 
-def _rotate(x: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
-    """``x: [B, H, T, hd]``; rotation of the two halves in fp32."""
-    t = x.shape[-2]
-    a, b = x.float().chunk(2, dim=-1)
-    c, s = cos[:t], sin[:t]
-    return torch.cat([a * c - b * s, b * c + a * s], dim=-1).to(x.dtype)
+class Attention(nn.Module):
+    """Causal multi-head attention: one fused QKV projection (one GEMM),
+    rotary positions, ``scaled_dot_product_attention`` on contiguous
+    ``[B, H, T, hd]`` operands, and the output projection."""
 
-
-class CausalSelfAttention(nn.Module):
     def __init__(self, cfg: ModelConfig) -> None:
         super().__init__()
-        self.n_heads, self.head_dim = cfg.n_heads, cfg.head_dim
-        self.q_proj = nn.Linear(cfg.d_model, cfg.d_model, bias=False)
-        self.k_proj = nn.Linear(cfg.d_model, cfg.d_model, bias=False)
-        self.v_proj = nn.Linear(cfg.d_model, cfg.d_model, bias=False)
-        self.o_proj = nn.Linear(cfg.d_model, cfg.d_model, bias=False)
+        self.heads, self.hd = cfg.n_heads, cfg.head_dim
+        self.qkv = nn.Linear(cfg.d_model, 3 * cfg.d_model, bias=False)
+        self.out = nn.Linear(cfg.d_model, cfg.d_model, bias=False)
 
-    def forward(self, x: Tensor, rope: tuple[Tensor, Tensor]) -> Tensor:
-        b, t, _ = x.shape
-
-        def heads(y: Tensor) -> Tensor:
-            # Contiguous [B, H, T, hd]: attention's math path never sees a
-            # transposed operand.
-            return y.view(b, t, self.n_heads, self.head_dim).transpose(1, 2).contiguous()
-
-        q = _rotate(heads(self.q_proj(x)), *rope)
-        k = _rotate(heads(self.k_proj(x)), *rope)
-        v = heads(self.v_proj(x))
+    def forward(self, x: Tensor, rotary: Rotary) -> Tensor:
+        b, t, d = x.shape
+        q, k, v = self.qkv(x).view(b, t, 3, self.heads, self.hd).unbind(2)
+        q, k = rotary(q), rotary(k)
+        q, k, v = (y.transpose(1, 2).contiguous() for y in (q, k, v))
         y = F.scaled_dot_product_attention(q, k, v, is_causal=True)
-        return self.o_proj(y.transpose(1, 2).reshape(b, t, -1))
+        return self.out(y.transpose(1, 2).reshape(b, t, d))
 
 
-class SwiGLU(nn.Module):
+class GatedMLP(nn.Module):
+    """SwiGLU: ``down(silu(gate x) * (up x))`` with gate and up as one GEMM."""
+
     def __init__(self, cfg: ModelConfig) -> None:
         super().__init__()
-        self.gate_proj = nn.Linear(cfg.d_model, cfg.d_ff, bias=False)
-        self.up_proj = nn.Linear(cfg.d_model, cfg.d_ff, bias=False)
-        self.down_proj = nn.Linear(cfg.d_ff, cfg.d_model, bias=False)
+        self.gate_up = nn.Linear(cfg.d_model, 2 * cfg.d_ff, bias=False)
+        self.down = nn.Linear(cfg.d_ff, cfg.d_model, bias=False)
 
-    def forward(self, x: Tensor, rope=None) -> Tensor:
-        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+    def forward(self, x: Tensor, rotary: Rotary | None = None) -> Tensor:
+        gate, up = self.gate_up(x).chunk(2, dim=-1)
+        return self.down(F.silu(gate) * up)
 
 
-class Sublayer(nn.Module):
-    def __init__(self, norm: RMSNorm, op: nn.Module) -> None:
+class DecoderLayer(nn.Module):
+    """Two sublayers, each a pre-norm and a transform: attention, then MLP."""
+
+    def __init__(self, cfg: ModelConfig) -> None:
         super().__init__()
-        self.norm = norm
-        self.op = op
+        self.attn_norm = RMSNorm(cfg.d_model, cfg.norm_eps)
+        self.attn = Attention(cfg)
+        self.mlp_norm = RMSNorm(cfg.d_model, cfg.norm_eps)
+        self.mlp = GatedMLP(cfg)
 
-    def forward(self, x: Tensor, rope) -> Tensor:
-        return self.op(self.norm(x), rope)
+    def sublayers(self):
+        yield self.attn_norm, self.attn
+        yield self.mlp_norm, self.mlp
 
 
 # --------------------------------------------------------------------------
-# The arena
+# Source staging
 # --------------------------------------------------------------------------
 
 
-def _alias(arena: Tensor, n_src: int) -> Tensor:
-    """``arena[:n_src]`` sharing storage but with its own version counter
-    (model.py:325-337)."""
-    view = torch.empty(0, dtype=arena.dtype, device=arena.device)
-    view.set_(arena.untyped_storage(), arena.storage_offset(), (n_src, *arena.shape[1:]), arena.stride())
-    return view
+class _Stream:
+    """The residual stream of one AttnRes forward: completed block
+    representations, the running sum, and (arena mode) the slot buffer that
+    mirrors them. ``holds[k]`` is the running-sum tensor whose bytes slot
+    ``k`` currently carries."""
 
-
-class _ArenaAttnRes(torch.autograd.Function):
-    """``impl(arena[:n_src], w)`` whose gradient flows to the live source
-    tensors (model.py:340-369). The operator's inner graph is built in forward
-    and replayed in backward; only the partial slot is restored first."""
-
-    @staticmethod
-    def forward(ctx, w, arena, n_src, has_partial, impl, eps, *sources):
-        with torch.enable_grad():
-            v = _alias(arena, n_src).requires_grad_(True)
-            q = w.detach().requires_grad_(True)
-            out = impl(v, q, eps)
-        ctx.inner = (v, q, out)
-        ctx.arena, ctx.n_src, ctx.has_partial = arena, n_src, has_partial
-        ctx.save_for_backward(*((sources[-1],) if has_partial else ()))
-        return out.detach()
-
-    @staticmethod
-    def backward(ctx, grad_out):
-        if ctx.has_partial:
+    def __init__(self, x0: Tensor, n_blocks: int, arena: bool) -> None:
+        self.blocks: list[Tensor] = [x0]
+        self.running: Tensor | None = None
+        self.slots: Tensor | None = None
+        self.holds: dict[int, Tensor] = {}
+        if arena:
+            self.slots = x0.new_empty((n_blocks + 1, *x0.shape))
             with torch.no_grad():
-                ctx.arena[ctx.n_src - 1].copy_(ctx.saved_tensors[0])
-        v, q, out = ctx.inner
-        ctx.inner = None
-        dv, dw = torch.autograd.grad(out, (v, q), grad_out)
-        return (dw, None, None, None, None, None, *(dv[j] for j in range(ctx.n_src)))
+                self.slots[0].copy_(x0)
+
+    def sources(self) -> list[Tensor]:
+        return self.blocks if self.running is None else [*self.blocks, self.running]
+
+    def accumulate(self, y: Tensor) -> None:
+        self.running = y if self.running is None else self.running + y
+        if self.slots is not None:
+            k = len(self.blocks)
+            with torch.no_grad():
+                self.slots[k].copy_(self.running)
+            self.holds[k] = self.running
+
+    def close_block(self) -> None:
+        self.blocks.append(self.running)
+        self.running = None
+
+    # -- eager sites: saved-tensor hooks over the slot buffer ----------------
+
+    def restore(self, k: int, value: Tensor) -> None:
+        if self.holds.get(k) is not value:
+            with torch.no_grad():
+                self.slots[k].copy_(value)
+            self.holds[k] = value
+
+    def saving(self, running: Tensor | None):
+        """Hooks under which an eager site may save views of the buffer."""
+        storage = self.slots.untyped_storage().data_ptr()
+        slot = len(self.blocks)
+
+        def pack(t: Tensor):
+            if running is not None and t.untyped_storage().data_ptr() == storage:
+                return (_BufferView, t, slot, running)
+            return t
+
+        def unpack(x):
+            if isinstance(x, tuple) and x and x[0] is _BufferView:
+                _, t, k, value = x
+                self.restore(k, value)
+                return t
+            return x
+
+        return torch.autograd.graph.saved_tensors_hooks(pack, unpack)
+
+
+class _BufferView(torch.autograd.Function):
+    """``slots[:n]`` as a differentiable function of the ``n`` live sources,
+    with no copy: the forward returns the prefix view, the backward hands each
+    source its slice of the gradient."""
+
+    @staticmethod
+    def forward(ctx, slots: Tensor, n: int, *sources: Tensor) -> Tensor:
+        return slots[:n]
+
+    @staticmethod
+    def backward(ctx, grad: Tensor):
+        return (None, None, *grad.unbind(0))
+
+
+class _SlotSiteHIP(torch.autograd.Function):
+    """One HIP site over the slot buffer. Forward: ``sy_fwd`` on the prefix
+    (source stride = one slot). Backward: ``sy_bwd_table`` with the
+    completed-block slots and the site's running-sum tensor as rows, and each
+    source's gradient as its own dv row."""
+
+    @staticmethod
+    def forward(ctx, q: Tensor, stream: _Stream, n: int, eps: float, *sources: Tensor) -> Tensor:
+        from . import _lib
+        from .hip_op import _ptr
+
+        slots = stream.slots
+        _, b, t, d = slots.shape
+        n_tok = b * t
+        q = q.contiguous()
+        out = slots.new_empty((b, t, d))
+        stats = torch.empty(2, n, n_tok, device=slots.device, dtype=torch.float32)
+        with torch.cuda.device(slots.device):
+            rc = _lib.lib().sy_fwd(_ptr(slots), _ptr(q), _ptr(out), _ptr(stats), n, n_tok, d, n_tok * d,
+                                   _lib.dtype_code(slots.dtype), _lib.dtype_code(q.dtype), float(eps),
+                                   _lib.stream_ptr(slots.device))
+        _lib.check(rc, "sy_fwd")
+        running = stream.running
+        ctx.stream, ctx.n, ctx.eps = stream, n, float(eps)
+        ctx.n_fixed = n - (1 if running is not None else 0)
+        ctx.save_for_backward(q, stats, *((running,) if running is not None else ()))
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out: Tensor):
+        from . import _lib
+        from .hip_op import _ptr
+
+        q, stats, *running = ctx.saved_tensors
+        stream, n = ctx.stream, ctx.n
+        slots = stream.slots
+        _, b, t, d = slots.shape
+        n_tok = b * t
+        dev, dt = slots.device, slots.dtype
+        grad_out = grad_out.to(dt).contiguous()
+        dv = torch.empty(n, b, t, d, device=dev, dtype=dt)
+        dq = torch.empty(d, device=dev, dtype=q.dtype)
+        lib = _lib.lib()
+        vt, wt = _lib.dtype_code(dt), _lib.dtype_code(q.dtype)
+        with torch.cuda.device(dev):
+            ws_bytes = lib.sy_bwd_workspace_bytes(n, n_tok, d, vt, wt)
+            if ws_bytes < 0:
+                _lib.check(int(ws_bytes), "sy_bwd_workspace_bytes")
+            ws = torch.empty(max(1, (ws_bytes + 3) // 4), device=dev, dtype=torch.float32)
+            st = _lib.stream_ptr(dev)
+            if n <= _lib.MAX_TABLE_ROWS:
+                rows = [slots[j] for j in range(ctx.n_fixed)] + running
+                rc = lib.sy_bwd_table(_lib.pointer_table(rows), _ptr(q), _ptr(grad_out), _ptr(stats),
+                                      _lib.pointer_table(dv.unbind(0)), _ptr(dq), _ptr(ws), ws.numel() * 4,
+                                      n, n_tok, d, vt, wt, ctx.eps, st)
+                what = "sy_bwd_table"
+            else:
+                if running:
+                    stream.restore(n - 1, running[0])
+                rc = lib.sy_bwd(_ptr(slots), _ptr(q), _ptr(grad_out), _ptr(stats), _ptr(dv), _ptr(dq),
+                                _ptr(ws), ws.numel() * 4, n, n_tok, d, n_tok * d, vt, wt, ctx.eps, st)
+                what = "sy_bwd"
+        _lib.check(rc, what)
+        return (dq, None, None, None, *dv.unbind(0))
+
+
+def _hip_stacked(v: Tensor, q: Tensor, eps: float) -> Tensor:
+    from .hip_op import block_attn_res_hip
+
+    return block_attn_res_hip(v, q, eps)
+
+
+def _hip_table(sources: list[Tensor], q: Tensor, eps: float) -> Tensor:
+    from .table_op import MAX_SOURCES, block_attn_res_sources
+
+    if len(sources) > MAX_SOURCES:
+        return _hip_stacked(torch.stack(sources), q, eps)
+    return block_attn_res_sources(sources, q, eps)
 
 
 # --------------------------------------------------------------------------
@@ -263,111 +413,115 @@ class _ArenaAttnRes(torch.autograd.Function):
 
 
 class Transformer(nn.Module):
+    """Decoder-only LM: embedding, ``n_layers`` decoder layers, final norm,
+    LM head (tied to the embedding by default). With an AttnRes mechanism,
+    ``attn_res[i]`` holds the pseudo-query and gain of site ``i``
+    (``n_sublayers`` sites plus the readout)."""
+
     def __init__(self, cfg: ModelConfig) -> None:
         super().__init__()
         self.cfg = cfg
         self.embed = nn.Embedding(cfg.vocab_size, cfg.d_model)
-        ops: list[nn.Module] = []
-        for _ in range(cfg.n_layers):
-            ops += [CausalSelfAttention(cfg), SwiGLU(cfg)]
-        self.sublayers = nn.ModuleList(Sublayer(RMSNorm(cfg.d_model, cfg.norm_eps), op) for op in ops)
-        # One pseudo-query and gain per sublayer plus the readout site; the
-        # modules carry parameters only, the operator comes from _IMPLS.
-        self.attn_res = (
-            nn.ModuleList(BlockAttnRes(cfg.d_model, eps=cfg.norm_eps) for _ in range(cfg.n_sublayers + 1))
-            if cfg.uses_attnres
-            else None
-        )
+        self.layers = nn.ModuleList(DecoderLayer(cfg) for _ in range(cfg.n_layers))
+        self.attn_res = (nn.ModuleList(BlockAttnRes(cfg.d_model, eps=cfg.norm_eps)
+                                       for _ in range(cfg.n_sublayers + 1))
+                         if cfg.uses_attnres else None)
         self.final_norm = RMSNorm(cfg.d_model, cfg.norm_eps)
         self.lm_head = nn.Linear(cfg.d_model, cfg.vocab_size, bias=False)
         if cfg.tie_embeddings:
             self.lm_head.weight = self.embed.weight
-        cos, sin = _rope_tables(cfg.max_seq_len, cfg.head_dim, cfg.rope_theta)
-        self.register_buffer("rope_cos", cos, persistent=False)
-        self.register_buffer("rope_sin", sin, persistent=False)
-        # Only Linear/Embedding draw from the RNG, so every mode built after the
-        # same seed shares identical weights (model.py:437-442).
-        for mod in self.modules():
-            if isinstance(mod, (nn.Linear, nn.Embedding)):
-                nn.init.normal_(mod.weight, mean=0.0, std=0.02)
-        depth_scale = 1.0 / math.sqrt(2 * cfg.n_layers)
-        with torch.no_grad():
-            for sub in self.sublayers:
-                proj = sub.op.o_proj if isinstance(sub.op, CausalSelfAttention) else sub.op.down_proj
-                proj.weight.mul_(depth_scale)
+        self.rotary = Rotary(cfg.head_dim, cfg.max_seq_len, cfg.rope_theta)
+        self._init_parameters()
         self.last_source_counts: list[int] = []
         self.last_alphas: list[Tensor] = []
+        #: Wrap staging and operator calls in profiler regions
+        #: (``attnres_stage``, ``attnres_op``) for attribution runs.
         self.profile_regions = False
+
+    def _init_parameters(self) -> None:
+        # N(0, 0.02) for every projection and the embedding, in module order;
+        # the AttnRes parameters (zeros, ones) draw nothing from the RNG, so a
+        # seed gives every residual mechanism the same shared weights. The
+        # projections that write into the residual stream are scaled by
+        # 1/sqrt(2 n_layers).
+        seen = set()
+        for mod in self.modules():
+            if isinstance(mod, (nn.Linear, nn.Embedding)) and id(mod.weight) not in seen:
+                seen.add(id(mod.weight))
+                nn.init.normal_(mod.weight, mean=0.0, std=0.02)
+        with torch.no_grad():
+            for layer in self.layers:
+                for proj in (layer.attn.out, layer.mlp.down):
+                    proj.weight.mul_(1.0 / math.sqrt(2 * self.cfg.n_layers))
 
     def param_counts(self) -> dict:
         total = sum(p.numel() for p in self.parameters())
-        attnres = sum(p.numel() for m in self.attn_res for p in m.parameters()) if self.attn_res is not None else 0
-        return {"total": total, "attnres": attnres, "non_attnres": total - attnres,
+        own = sum(p.numel() for p in self.attn_res.parameters()) if self.attn_res is not None else 0
+        return {"total": total, "attnres": own, "non_attnres": total - own,
                 "embedding": self.embed.weight.numel(), "tied_head": self.cfg.tie_embeddings}
 
+    def _sublayers(self):
+        for layer in self.layers:
+            yield from layer.sublayers()
+
     def forward(self, idx: Tensor, targets: Tensor | None = None, collect_alphas: bool = False):
-        _, t = idx.shape
-        if t > self.cfg.max_seq_len:
-            raise ValueError(f"sequence length {t} exceeds max_seq_len {self.cfg.max_seq_len}")
-        rope = (self.rope_cos[:t], self.rope_sin[:t])
-        x0 = self.embed(idx)
+        """``idx [B, T]`` -> logits ``[B, T, V]``, or ``(logits, loss)`` with
+        ``targets``. ``collect_alphas`` records each site's mean attention
+        weight per source in ``last_alphas`` (a diagnostic; it costs time)."""
+        if idx.shape[1] > self.cfg.max_seq_len:
+            raise ValueError(f"sequence length {idx.shape[1]} exceeds max_seq_len {self.cfg.max_seq_len}")
+        x = self.embed(idx)
         self.last_alphas = []
-        h = self._forward_attnres(x0, rope, collect_alphas) if self.cfg.uses_attnres else self._forward_standard(x0, rope)
+        if self.cfg.uses_attnres:
+            h = self._attnres_stream(x, collect_alphas)
+        else:
+            for norm, fn in self._sublayers():
+                x = x + fn(norm(x), self.rotary)
+            self.last_source_counts = []
+            h = x
         logits = self.lm_head(self.final_norm(h))
         if targets is None:
             return logits
         return logits, F.cross_entropy(logits.float().flatten(0, 1), targets.flatten())
 
-    def _forward_standard(self, x: Tensor, rope) -> Tensor:
-        for sub in self.sublayers:
-            x = x + sub(x, rope)
-        self.last_source_counts = []
-        return x
-
-    def _forward_attnres(self, x0: Tensor, rope, collect_alphas: bool) -> Tensor:
+    def _attnres_stream(self, x0: Tensor, collect_alphas: bool) -> Tensor:
         cfg = self.cfg
-        b, t, d = x0.shape
-        arena = None
-        if cfg.sources == "arena":
-            # Fresh per forward: a second forward before backward must not
-            # overwrite the first one's saved slots.
-            arena = torch.empty(cfg.n_blocks + 1, b, t, d, device=x0.device, dtype=x0.dtype)
-            with torch.no_grad():
-                arena[0].copy_(x0)
-        blocks: list[Tensor] = [x0]
-        partial: Tensor | None = None
-        counts: list[int] = []
-        for i, sub in enumerate(self.sublayers):
-            if i and i % cfg.block_size == 0:
-                blocks.append(partial)  # already sitting in its arena slot
-                partial = None
-            sources = blocks if partial is None else [*blocks, partial]
-            counts.append(len(sources))
-            h = self._site(i, arena, sources, partial is not None, collect_alphas)
-            y = sub(h, rope)
-            partial = y if partial is None else partial + y
-            if arena is not None:
-                with self._region("attnres_stage"), torch.no_grad():
-                    arena[len(blocks)].copy_(partial)
-        blocks.append(partial)
-        counts.append(len(blocks))
-        self.last_source_counts = counts
-        return self._site(len(self.sublayers), arena, blocks, False, collect_alphas)
-
-    def _site(self, i: int, arena: Tensor | None, sources: list[Tensor], has_partial: bool,
-              collect_alphas: bool) -> Tensor:
-        site = self.attn_res[i]
-        q = site.effective_query()
-        impl = _IMPLS[self.cfg.residual]
-        if collect_alphas:
-            self.last_alphas.append(_mean_alpha(sources, q, self.cfg.norm_eps))
-        if arena is None:
+        stream = _Stream(x0, cfg.n_blocks, arena=cfg.sources == "arena")
+        counts = []
+        for i, (norm, fn) in enumerate(self._sublayers()):
+            if i > 0 and i % cfg.block_size == 0:
+                stream.close_block()
+            h = self._site(i, stream, collect_alphas)
+            counts.append(len(stream.sources()))
+            y = fn(norm(h), self.rotary)
             with self._region("attnres_stage"):
-                v = torch.stack(sources, 0)
+                stream.accumulate(y)
+        stream.close_block()
+        counts.append(len(stream.sources()))
+        self.last_source_counts = counts
+        return self._site(cfg.n_sublayers, stream, collect_alphas)
+
+    def _site(self, i: int, stream: _Stream, collect_alphas: bool) -> Tensor:
+        cfg = self.cfg
+        q = self.attn_res[i].effective_query()
+        sources = stream.sources()
+        n = len(sources)
+        if collect_alphas:
+            self.last_alphas.append(_mean_alpha(sources, q, cfg.norm_eps))
+        hip = cfg.residual == "switchyard"
+        if cfg.sources == "stack":
+            with self._region("attnres_stage"):
+                v = torch.stack(sources)
             with self._region("attnres_op"):
-                return impl(v, q, self.cfg.norm_eps)
+                return _hip_stacked(v, q, cfg.norm_eps) if hip else folded_form(v, q, cfg.norm_eps)
+        if cfg.sources == "table":
+            with self._region("attnres_op"):
+                return _hip_table(sources, q, cfg.norm_eps)
         with self._region("attnres_op"):
-            return _ArenaAttnRes.apply(q, arena, len(sources), has_partial, impl, self.cfg.norm_eps, *sources)
+            if hip:
+                return _SlotSiteHIP.apply(q, stream, n, cfg.norm_eps, *sources)
+            with stream.saving(stream.running):
+                return folded_form(_BufferView.apply(stream.slots, n, *sources), q, cfg.norm_eps)
 
     def _region(self, name: str):
         return torch.profiler.record_function(name) if self.profile_regions else contextlib.nullcontext()
@@ -375,7 +529,9 @@ class Transformer(nn.Module):
 
 @torch.no_grad()
 def _mean_alpha(sources: list[Tensor], q: Tensor, eps: float) -> Tensor:
-    """Mean attention weight per source over batch and positions (model.py:571-581)."""
-    v = torch.stack(sources, 0).float()
-    keys = v * torch.rsqrt(v.pow(2).mean(-1, keepdim=True) + eps)
-    return torch.einsum("d,nbtd->nbt", q.float(), keys).softmax(0).mean(dim=(1, 2))
+    """Mean softmax weight of each source over batch and positions, in fp32
+    (the reference's diagnostic, model.py:571-581)."""
+    logits = torch.stack([
+        (s.float() @ q.float()) * s.float().square().mean(-1).add(eps).rsqrt() for s in sources
+    ])
+    return logits.softmax(0).mean(dim=(1, 2))

@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define SY_ABI_VERSION 2
+#define SY_ABI_VERSION 3
 
 /* Most sources a per-source pointer list (the *_table entry points) may hold. */
 #define SY_MAX_TABLE_ROWS 16
@@ -108,7 +108,7 @@ int sy_plan_for(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int 
 
 /* sy_plan_for for a launch of n_tok tokens on the current device: for the
  * forward and the backward, the tile sy_fwd / sy_bwd run, with the token-count
- * rule and the SY_TILE_* measurement override applied; other ops as
+ * rule and any sy_tuning_set tile override applied; other ops as
  * sy_plan_for. Without a device the token-count rule is skipped. No
  * counterpart in the reference, whose launch configuration ignores the token
  * count (src/switchyard/triton_op.py:130-150); it serves benchmarks and
@@ -268,6 +268,35 @@ int64_t sy_probe_grid(int64_t bytes);
  * tokens. Diagnostics only; no reference counterpart. */
 int sy_kernel_info(int op, int64_t n_src, int64_t n_tok, int64_t d, int v_dtype, int w_dtype,
                    int32_t out[4]);
+
+/* Measurement-only overrides of the launch configuration. The library never
+ * reads its environment: the kernel, tile and grid of every call are a
+ * function of shape, dtype, alignment and device, unless a caller installs
+ * overrides here. A tile triple {W, VPL, NR} of zeros keeps the planner's
+ * choice; a triple is applied only where that tile is built, covers the row
+ * and (backward, batched) holds every source, and is otherwise ignored.
+ * bwd_blocks_per_cu (1..64) replaces the backward's persistent workgroups per
+ * CU -- and with it the dw partial-row count and dw's bits. mx_slots (1 or 2)
+ * sets the token slots of the matrix-core batched forward; bmx_waves = 4 runs
+ * the four-wave matrix-core batched backward. The overrides are process-wide
+ * and apply to calls issued after sy_tuning_set returns; they exist for tile
+ * sweeps and for tests that force a tile. No reference counterpart (the
+ * reference's tile constants are module globals, triton_op.py:120-150). */
+typedef struct sy_tuning {
+  int32_t fwd_tile[3];
+  int32_t bwd_tile[3];
+  int32_t batched_tile[3];
+  int32_t sol_tile[3];
+  int32_t bwd_blocks_per_cu;
+  int32_t mx_slots;
+  int32_t bmx_waves;
+} sy_tuning;
+
+/* Install overrides (NULL restores the defaults). SY_ERR_SHAPE for a value
+ * out of range, which leaves the previous overrides in place. */
+int sy_tuning_set(const sy_tuning* t);
+/* Copy the installed overrides (all zeros when none). */
+int sy_tuning_get(sy_tuning* out);
 
 /* Static string for a status code (negative sy_status or positive hipError_t). */
 const char* sy_strerror(int code);

@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_strings():
     lib = _lib.lib()
-    assert lib.sy_abi_version() == 2
+    assert lib.sy_abi_version() == 3
     for code in (OK, NULL, SHAPE, DTYPE, WORKSPACE, STRIDE, DEVICE, OP):
         assert lib.sy_strerror(code)
     assert b"NULL" in lib.sy_strerror(NULL)
@@ -328,3 +328,51 @@ def test_plan_for_tokens_checks_input_and_matches_the_plan_without_a_device():
         assert lib.sy_plan_for_tokens(op, 9, 0, 512, 2048, BF16, BF16, 1, ctypes.byref(p)) == OK
         assert lib.sy_plan_for(op, 9, 0, 2048, BF16, BF16, 1, ctypes.byref(q)) == OK
         assert p.as_dict() == q.as_dict()
+
+
+# -- measurement overrides ---------------------------------------------------
+
+
+def test_no_overrides_are_installed_by_default():
+    t = _lib.Tuning()
+    assert _lib.lib().sy_tuning_get(ctypes.byref(t)) == OK
+    assert all(getattr(t, f)[k] == 0 for f in ("fwd_tile", "bwd_tile", "batched_tile", "sol_tile")
+               for k in range(3))
+    assert (t.bwd_blocks_per_cu, t.mx_slots, t.bmx_waves) == (0, 0, 0)
+
+
+def test_environment_does_not_change_the_launch(monkeypatch):
+    """The library reads no environment variables: the names round one used
+    for its measurement knobs are inert now."""
+    base = _lib.plan(_lib.OP_FWD, 9, 2048, torch.bfloat16, n_tok=4096)
+    for name, val in (("SY_TILE_FWD", "2,2,9"), ("SY_TILE_BWD", "2,2,9"), ("SY_BWD_BLOCKS_PER_CU", "3"),
+                      ("SY_MX_SLOTS", "1"), ("SY_BMX_WAVES", "4")):
+        monkeypatch.setenv(name, val)
+    assert _lib.plan(_lib.OP_FWD, 9, 2048, torch.bfloat16, n_tok=4096) == base
+
+
+def test_tuning_overrides_the_launched_tile_and_restores():
+    base = _lib.plan(_lib.OP_FWD, 9, 2048, torch.bfloat16, n_tok=4096)
+    with _lib.tuning(fwd_tile=(2, 2, 9)):
+        p = _lib.plan(_lib.OP_FWD, 9, 2048, torch.bfloat16, n_tok=4096)
+        assert (p["waves_per_token"], p["chunks_per_lane"], p["rows_per_tile"]) == (2, 2, 9)
+        # a tile that does not cover the row is ignored
+        with _lib.tuning(fwd_tile=(1, 1, 9)):
+            assert _lib.plan(_lib.OP_FWD, 9, 2048, torch.bfloat16, n_tok=4096) == base
+        p = _lib.plan(_lib.OP_FWD, 9, 2048, torch.bfloat16, n_tok=4096)
+        assert p["waves_per_token"] == 2
+        # sy_plan_for never applies overrides
+        assert _lib.plan(_lib.OP_FWD, 9, 2048, torch.bfloat16)["waves_per_token"] == 1
+    assert _lib.plan(_lib.OP_FWD, 9, 2048, torch.bfloat16, n_tok=4096) == base
+
+
+@pytest.mark.parametrize("field,val", [("bwd_blocks_per_cu", 65), ("mx_slots", 3), ("bmx_waves", 8),
+                                       ("bwd_blocks_per_cu", -1)])
+def test_tuning_rejects_out_of_range_values(field, val):
+    t = _lib.Tuning()
+    setattr(t, field, val)
+    assert _lib.lib().sy_tuning_set(ctypes.byref(t)) == SHAPE
+    got = _lib.Tuning()
+    assert _lib.lib().sy_tuning_get(ctypes.byref(got)) == OK
+    assert getattr(got, field) == 0
+    assert _lib.lib().sy_tuning_get(None) == NULL

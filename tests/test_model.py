@@ -79,6 +79,13 @@ def test_attnres_adds_only_the_parameters_the_paper_says():  # :175-182
     assert sum(p.numel() for p in att.parameters()) - std == 2 * att.cfg.d_model * (att.cfg.n_sublayers + 1)
 
 
+def test_table_sources_need_the_hip_operator():
+    with pytest.raises(ValueError, match="table"):
+        ModelConfig(residual="attnres", sources="table")
+    ModelConfig(residual="switchyard", sources="table")
+    assert slab_copies(48, 8, "table") == 0
+
+
 def test_config_rejects_bad_structure():
     with pytest.raises(ValueError, match="residual"):
         ModelConfig(residual="nope")
@@ -131,18 +138,38 @@ def test_framework_modes_overfit_a_fixed_batch(residual):  # :190-208
 
 @pytest.mark.gpu
 @pytest.mark.skipif(not HAS_GPU, reason="needs a HIP device")
-def test_arena_and_stack_agree_with_the_hip_operator():
+@pytest.mark.parametrize("sources", ["arena", "table"])
+def test_source_modes_agree_with_stacking_for_the_hip_operator(sources):
     idx, tgt = _batch("cuda")
     outs = {}
-    for sources in ("stack", "arena"):
-        m = _build("switchyard", sources, "cuda")
+    for mode in ("stack", sources):
+        m = _build("switchyard", mode, "cuda")
         logits, loss = m(idx, tgt)
         loss.backward()
-        outs[sources] = (loss, logits, _grads(m))
-    # Same bytes reach the operator in the same layout: bitwise forward.
+        outs[mode] = (loss, logits, _grads(m))
+    # Same source rows reach the same kernels: bitwise forward.
+    torch.testing.assert_close(outs[sources][0], outs["stack"][0], rtol=0, atol=0)
+    torch.testing.assert_close(outs[sources][1], outs["stack"][1], rtol=0, atol=0)
+    ga, gs = outs[sources][2], outs["stack"][2]
+    assert ((ga - gs).norm() / gs.norm()).item() < 1e-6
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not HAS_GPU, reason="needs a HIP device")
+def test_arena_with_more_sources_than_the_table_holds():
+    """17 sources at the readout site: the arena's HIP backward restores the
+    running-sum slot and takes the stacked path instead of the table."""
+    idx, tgt = _batch("cuda", t=16)
+    outs = {}
+    for mode in ("stack", "arena"):
+        torch.manual_seed(0)
+        m = Transformer(_cfg(residual="switchyard", sources=mode, n_layers=16, n_blocks=16)).cuda()
+        logits, loss = m(idx, tgt)
+        loss.backward()
+        assert max(m.last_source_counts) == 17
+        outs[mode] = (loss, _grads(m))
     torch.testing.assert_close(outs["arena"][0], outs["stack"][0], rtol=0, atol=0)
-    torch.testing.assert_close(outs["arena"][1], outs["stack"][1], rtol=0, atol=0)
-    ga, gs = outs["arena"][2], outs["stack"][2]
+    ga, gs = outs["arena"][1], outs["stack"][1]
     assert ((ga - gs).norm() / gs.norm()).item() < 1e-6
 
 

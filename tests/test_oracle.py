@@ -331,6 +331,72 @@ def test_c_stats_merge_and_batched_agree_with_torch():
                                batched_folded_form(v, q)[:, 0].numpy(), rtol=1e-12, atol=1e-12)
 
 
+def _stats_by_definition(v, w, eps=DEFAULT_EPS):
+    """``(o, m, l)`` of one token set from the definitions, with plain Python
+    loops: m is the largest logit, l the sum of exp(logit - m), o the
+    exp(logit - m)-weighted sum of the raw sources."""
+    n, t, d = len(v), len(v[0]), len(w)
+    o = [[0.0] * d for _ in range(t)]
+    m, ell = [0.0] * t, [0.0] * t
+    for j in range(t):
+        logits = []
+        for k in range(n):
+            row = v[k][j]
+            r = 1.0 / math.sqrt(sum(x * x for x in row) / d + eps)
+            logits.append(r * sum(a * b for a, b in zip(w, row)))
+        m[j] = max(logits)
+        ps = [math.exp(z - m[j]) for z in logits]
+        ell[j] = sum(ps)
+        for k in range(n):
+            for c in range(d):
+                o[j][c] += ps[k] * v[k][j][c]
+    return np.array(o), np.array(m), np.array(ell)
+
+
+def test_stats_follow_their_definitions():
+    """m, l and o of both restatements against the definitions, on a token
+    set where row 2 of token 0 is the query direction scaled by 3, so the
+    largest logit is known in closed form: c ||w|| / sqrt(c^2 / D + eps)."""
+    v, w = _inputs(n=4, b=1, t=3, d=10, seed=5, scale=2.0)
+    v = v[:, 0].clone()
+    v[2, 0] = 3.0 * w / w.norm()
+    o_def, m_def, l_def = _stats_by_definition(v.tolist(), w.tolist())
+    want = 3.0 * w.norm().item() / math.sqrt(9.0 / 10 + DEFAULT_EPS)
+    assert math.isclose(m_def[0], want, rel_tol=1e-13)
+    oc, mc, lc = c_oracle.attn_with_stats(v.numpy(), w.numpy())
+    ot, mt, lt = attn_with_stats(v[:, None], w)
+    for got in ((oc, mc, lc), (ot[0].numpy(), mt[0].numpy(), lt[0].numpy())):
+        np.testing.assert_allclose(got[0], o_def, rtol=1e-12, atol=1e-12)
+        np.testing.assert_allclose(got[1], m_def, rtol=1e-13, atol=0)
+        np.testing.assert_allclose(got[2], l_def, rtol=1e-12, atol=0)
+    assert mc[0] == pytest.approx(want, rel=1e-13)
+
+
+def test_config1_eager_fp32_is_within_the_reference_tolerance():
+    """BASELINE config 1 (the reference's CPU plumbing case): N=4 B=1 T=256
+    D=512 fp32, seed 0, v ~ N(0,1), w ~ N(0, 0.5), grad_out ~ N(0,1),
+    eps 1e-6. The product's eager ``folded_form`` in fp32, forward and
+    backward through torch.autograd, against the float64 oracle: rel-L2 at
+    most 1e-5 (the reference's fp32 tolerance, bench/bench_operator.py:289)."""
+    from switchyard.baselines import folded_form as eager
+
+    gen = torch.Generator().manual_seed(0)
+    v = torch.randn(4, 1, 256, 512, generator=gen)
+    w = 0.5 * torch.randn(512, generator=gen)
+    g = torch.randn(1, 256, 512, generator=gen)
+    vv, ww = v.clone().requires_grad_(True), w.clone().requires_grad_(True)
+    out = eager(vv, ww, 1e-6)
+    out.backward(g)
+    o64 = block_attn_res_oracle(v, w)
+    dv64, dw64 = oracle_grads(v, w, g)
+    for got, ref in ((out, o64), (vv.grad, dv64), (ww.grad, dw64)):
+        assert got.dtype == torch.float32
+        assert rel_l2(got, ref) <= 1e-5
+    # the C restatement agrees with the torch oracle on this case too
+    oc = c_oracle.forward(v[:, 0].double().numpy(), w.double().numpy())
+    np.testing.assert_allclose(oc, o64[0].numpy(), rtol=1e-10, atol=1e-12)
+
+
 # --------------------------------------------------------------------------
 # 5. Golden fixtures
 # --------------------------------------------------------------------------

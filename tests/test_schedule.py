@@ -267,17 +267,18 @@ def test_batched_matrix_kernel(nstd, dtype):
 
 
 @pytest.mark.parametrize("t", [777, 3])
-def test_batched_matrix_slots_agree(monkeypatch, t):
-    """Two token slots per workgroup and one (the SY_MX_SLOTS measurement
-    knob) give the same bits: the slots only change which workgroup computes
-    a token. Three tokens forced onto two slots leave the second workgroup's
-    second slot empty."""
+def test_batched_matrix_slots_agree(t):
+    """Two token slots per workgroup and one (the mx_slots measurement
+    override of sy_tuning_set) give the same bits: the slots only change which
+    workgroup computes a token. Three tokens forced onto two slots leave the
+    second workgroup's second slot empty."""
+    from switchyard import _lib
+
     v, _ = _make(9, t, 2048, torch.bfloat16, seed=23)
     q = (torch.randn(8, 2048, generator=torch.Generator().manual_seed(24)) * 0.5).to(torch.bfloat16).to(DEV)
     outs = []
-    for slots in ("2", "1"):
-        monkeypatch.setenv("SY_MX_SLOTS", slots)
-        with torch.no_grad():
+    for slots in (2, 1):
+        with _lib.tuning(mx_slots=slots), torch.no_grad():
             outs.append(block_attn_res_batched_with_stats(v, q))
     for a, b in zip(*outs):
         assert torch.equal(a, b)

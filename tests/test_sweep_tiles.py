@@ -1,0 +1,88 @@
+"""The tiles the shape sweeps time, checked at the shapes that select them (GPU).
+
+Which register tile a launch runs depends on N, D and (below three tokens per
+CU) the token count, so a test at a small T can exercise a different kernel
+from the one a sweep times. These cases run the sweep shapes themselves -- or,
+for the D sweep, the same tile at a token count above four per CU -- assert
+through ``sy_plan_for_tokens`` which tile the launch takes, and compare the
+forward output, dv and dw with the float64 C oracle at the 1.10x dtype-floor
+bar. If a future planner change moves a shape onto another tile, the tile
+assertion fails before the numbers are compared.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+if not torch.cuda.is_available():  # pragma: no cover
+    pytest.skip("needs a HIP device", allow_module_level=True)
+
+from oracle import c_oracle  # noqa: E402
+from oracle.reference import dtype_floor, rel_l2  # noqa: E402
+from switchyard import _lib  # noqa: E402
+from switchyard.hip_op import block_attn_res_hip  # noqa: E402
+
+DEV = "cuda"
+CUS = torch.cuda.get_device_properties(0).multi_processor_count
+
+
+def _tile(op, n, d, dtype, n_tok):
+    p = _lib.plan(op, n, d, dtype, n_tok=n_tok)
+    return p["family_name"], (p["waves_per_token"], p["chunks_per_lane"], p["rows_per_tile"])
+
+
+def _check(n, b, t, d, dtype, seed):
+    gen = torch.Generator().manual_seed(seed)
+    v = torch.randn(n, b, t, d, generator=gen).to(dtype)
+    w = (0.5 * torch.randn(d, generator=gen)).to(dtype)
+    g = torch.randn(b, t, d, generator=gen).to(dtype)
+    vv = v.to(DEV).requires_grad_(True)
+    ww = w.to(DEV).requires_grad_(True)
+    out = block_attn_res_hip(vv, ww)
+    out.backward(g.to(DEV))
+    torch.cuda.synchronize()
+    n_tok = b * t
+    v64 = v.double().reshape(n, n_tok, d).numpy()
+    ro = torch.from_numpy(c_oracle.forward(v64, w.double().numpy()))
+    rdv, rdw = c_oracle.backward(v64, w.double().numpy(), g.double().reshape(n_tok, d).numpy())
+    res = {}
+    for name, got, ref in (("out", out.detach().reshape(n_tok, d), ro),
+                           ("dv", vv.grad.reshape(n, n_tok, d), torch.from_numpy(rdv)),
+                           ("dw", ww.grad, torch.from_numpy(rdw))):
+        err, floor = rel_l2(got.cpu(), ref), dtype_floor(ref, dtype)
+        res[name] = err / floor
+        assert err <= 1.10 * floor, f"{name}: rel_l2 {err:.4e} vs floor {floor:.4e}"
+    return res
+
+
+# (n, b, t, d): expected (forward family, tile), (backward tile)
+SWEEP_CASES = [
+    # N sweep, B=1 T=4096 D=2048 (config 4)
+    ((2, 1, 4096, 2048), ("resident", (1, 4, 4)), (2, 2, 4)),
+    ((4, 1, 4096, 2048), ("resident", (1, 4, 4)), (2, 2, 4)),
+    ((16, 1, 4096, 2048), ("chunked", (1, 4, 4)), (1, 4, 16)),
+    # N between the sweep points: the 16-row backward with a partly filled tile
+    ((12, 1, 4 * 256, 2048), ("chunked", (1, 4, 4)), (1, 4, 16)),
+    # D sweep tiles (config 4 uses B=4 T=4096; the tile depends only on the
+    # token count being above two per CU)
+    ((9, 4, 256, 1024), ("resident", (1, 2, 9)), (1, 2, 9)),
+    ((9, 4, 256, 4096), ("resident", (2, 4, 9)), (2, 4, 9)),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("shape,fwd,bwd", SWEEP_CASES, ids=[f"N{s[0]}B{s[1]}T{s[2]}D{s[3]}" for s, _, _ in SWEEP_CASES])
+def test_sweep_shape_runs_its_tile_at_the_oracle_floor(shape, fwd, bwd, dtype):
+    n, b, t, d = shape
+    if shape == (12, 1, 4 * 256, 2048):
+        t = 4 * CUS  # four tokens per CU on any device
+    n_tok = b * t
+    assert n_tok > 2 * CUS, "the token-count rule would pick another tile"
+    print(f"sweep tile N={n} B={b} T={t} D={d} {dtype}: expect fwd {fwd} bwd {bwd}", flush=True)
+    assert _tile(_lib.OP_FWD, n, d, dtype, n_tok) == fwd
+    assert _tile(_lib.OP_BWD, n, d, dtype, n_tok) == ("resident", bwd)
+    res = _check(n, b, t, d, dtype, seed=100 + n + d // 512)
+    print(f"  ratios to the floor: {res}", flush=True)

@@ -2,8 +2,8 @@
 runs (4,1,NR) up to one token per CU and (2,2,NR) up to two, the backward
 (4,1,NR); above that the plan's one-wave tiles. Each case checks, bit for bit,
 that the default launch equals the launch forced onto the expected tile with
-the SY_TILE_* measurement override, and that the result matches the float64
-oracle. Token counts are derived from the device's CU count.
+the measurement override of sy_tuning_set, and that the result matches the
+float64 oracle. Token counts are derived from the device's CU count.
 """
 
 from __future__ import annotations
@@ -44,15 +44,14 @@ def _run(n, t, d, seed, dtype=torch.bfloat16):
     (16, 2, "2,2,16", "4,1,16", torch.bfloat16),
     (9, 4, "1,4,9", "1,4,9", torch.bfloat16),
 ])
-def test_default_launch_takes_the_rule_tile(monkeypatch, n, per_cu, fwd_tile, bwd_tile, dtype):
+def test_default_launch_takes_the_rule_tile(n, per_cu, fwd_tile, bwd_tile, dtype):
+    from switchyard import _lib
+
     t, d = CUS * per_cu, 2048
     print(f"token rule N={n} T={t} {dtype} expect fwd {fwd_tile} bwd {bwd_tile}", flush=True)
-    monkeypatch.delenv("SY_TILE_FWD", raising=False)
-    monkeypatch.delenv("SY_TILE_BWD", raising=False)
     ins, got = _run(n, t, d, seed=n + per_cu, dtype=dtype)
-    monkeypatch.setenv("SY_TILE_FWD", fwd_tile)
-    monkeypatch.setenv("SY_TILE_BWD", bwd_tile)
-    _, forced = _run(n, t, d, seed=n + per_cu, dtype=dtype)
+    with _lib.tuning(fwd_tile=map(int, fwd_tile.split(",")), bwd_tile=map(int, bwd_tile.split(","))):
+        _, forced = _run(n, t, d, seed=n + per_cu, dtype=dtype)
     for a, b, what in zip(got, forced, ("out", "dv", "dw")):
         assert torch.equal(a, b), what
     v, w, go = ins
@@ -66,11 +65,9 @@ def test_default_launch_takes_the_rule_tile(monkeypatch, n, per_cu, fwd_tile, bw
 
 @pytest.mark.parametrize("per_cu,fwd_tile,bwd_tile", [(1, (4, 1, 9), (4, 1, 9)), (2, (2, 2, 9), (4, 1, 9)),
                                                       (16, (1, 4, 9), (1, 4, 9))])
-def test_plan_for_tokens_reports_the_launched_tile(monkeypatch, per_cu, fwd_tile, bwd_tile):
+def test_plan_for_tokens_reports_the_launched_tile(per_cu, fwd_tile, bwd_tile):
     from switchyard import _lib
 
-    monkeypatch.delenv("SY_TILE_FWD", raising=False)
-    monkeypatch.delenv("SY_TILE_BWD", raising=False)
     for op, want in ((_lib.OP_FWD, fwd_tile), (_lib.OP_BWD, bwd_tile)):
         p = _lib.plan(op, 9, 2048, torch.bfloat16, n_tok=CUS * per_cu)
         assert (p["waves_per_token"], p["chunks_per_lane"], p["rows_per_tile"]) == want
