@@ -9,6 +9,11 @@
 #include "../../include/switchyard.h"
 #include "sy_launch.hpp"
 
+// Workspace of sy_bwd_static: the dw partial rows of callers that cannot
+// allocate. One copy per GPU, at that GPU's own address; host code uses the
+// address hipGetSymbolAddress returns for the current device, never this name.
+static __device__ __align__(256) float scratch[SY_STATIC_WORKSPACE_BYTES / sizeof(float)];
+
 namespace sy {
 
 namespace {
@@ -26,6 +31,11 @@ int status(hipError_t e) { return e == hipSuccess ? SY_OK : (int)e; }
 
 std::mutex g_mu;
 std::map<int, int> g_cus;                                   // device -> CU count
+
+// Device address of `scratch` per device (resolved on the first sy_bwd_static
+// call on that device, with the device current).
+std::mutex g_scratch_mu;
+std::map<int, void*> g_scratch;
 
 // Measurement overrides (sy_tuning_set). g_tuning_on is read on every launch
 // without the lock; the struct itself only under it.
@@ -228,6 +238,26 @@ int listed_rows(const void* const* rows, int64_t n_src, RowTable* t, bool* rows_
 }
 
 }  // namespace
+
+// The current device's copy of `scratch`. Errors: SY_ERR_DEVICE without a
+// device, or the hipError_t of the symbol lookup.
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e == hipErrorNoDevice ? SY_ERR_DEVICE : (int)e;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  auto it = g_scratch.find(dev);
+  if (it != g_scratch.end()) {
+    *out = it->second;
+    return SY_OK;
+  }
+  void* p = nullptr;
+  e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || p == nullptr) return e != hipSuccess ? (int)e : SY_ERR_DEVICE;
+  g_scratch[dev] = p;
+  *out = p;
+  return SY_OK;
+}
 
 bool tuning_snapshot(sy_tuning* out) {
   if (!g_tuning_on.load(std::memory_order_acquire)) return false;
@@ -471,6 +501,32 @@ int sy_bwd(const void* v, const void* w, const void* grad_out, const float* stat
   const RowTable td = stacked(dv, n_src, n_tok * d, v_dtype, &dok);
   return bwd_impl(tv, vok, w, grad_out, stats, nullptr, nullptr, td, dok, false, dw, workspace,
                   workspace_bytes, n_src, n_tok, d, v_dtype, w_dtype, eps, (hipStream_t)stream);
+}
+
+int sy_bwd_static(const void* v, const void* w, const void* grad_out, const float* stats, void* dv,
+                  void* dw, int64_t n_src, int64_t n_tok, int64_t d, int64_t src_stride, int v_dtype,
+                  int w_dtype, float eps, void* stream) {
+  if (dw == nullptr) return SY_ERR_NULL;
+  if (n_tok != 0 && (v == nullptr || w == nullptr || grad_out == nullptr || dv == nullptr))
+    return SY_ERR_NULL;
+  int rc = check_common(n_src, n_tok, d, src_stride, v_dtype, w_dtype);
+  if (rc != SY_OK) return rc;
+  if (n_tok != 0) {
+    // The size the array must hold, as sy_bwd_workspace_bytes reports it.
+    int rows = 0;
+    rc = workspace_rows(n_src, n_tok, d, v_dtype, w_dtype, &rows);
+    if (rc != SY_OK) return rc;
+    if ((int64_t)rows * d * (int64_t)sizeof(float) > SY_STATIC_WORKSPACE_BYTES) return SY_ERR_WORKSPACE;
+  }
+  void* ws = nullptr;
+  rc = scratch_address(&ws);
+  if (rc != SY_OK) return rc;
+  bool vok = false, dok = false;
+  const RowTable tv = stacked(v, n_src, src_stride, v_dtype, &vok);
+  const RowTable td = stacked(dv, n_src, n_tok * d, v_dtype, &dok);
+  return bwd_impl(tv, vok, w, grad_out, stats, nullptr, nullptr, td, dok, false, dw, ws,
+                  SY_STATIC_WORKSPACE_BYTES, n_src, n_tok, d, v_dtype, w_dtype, eps,
+                  (hipStream_t)stream);
 }
 
 int sy_bwd_table(const void* const* v_rows, const void* w, const void* grad_out,

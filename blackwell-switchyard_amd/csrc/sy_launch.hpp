@@ -202,6 +202,8 @@ hipError_t launch_bwd_batched_matrix(const BwdBatchedArgs& a, int grid, hipStrea
 
 // Device queries, cached per device (sy_capi.cpp).
 hipError_t cu_count(int* out);
+// Device address of sy_bwd_static's workspace on the current device.
+int scratch_address(void** out);
 
 // Register/LDS footprint of one kernel instantiation, the workgroups per CU
 // that footprint allows, and (when filled by a launcher) the launch grid.

@@ -84,6 +84,8 @@ SIGNATURES = {
     "sy_fwd_batched": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32, ctypes.c_float, _vp]),
     "sy_sol": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp]),
     "sy_fwd_table": (_i32, [_vpp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, ctypes.c_float, _vp]),
+    "sy_bwd_static": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32,
+                             ctypes.c_float, _vp]),
     "sy_bwd_table": (_i32, [_vpp, _vp, _vp, _vp, _vpp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32,
                             ctypes.c_float, _vp]),
     "sy_fwd_batched_table": (_i32, [_vpp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, ctypes.c_float,

@@ -182,6 +182,23 @@ int sy_bwd_table(const void* const* v_rows, const void* w, const void* grad_out,
                  int64_t workspace_bytes, int64_t n_src, int64_t n_tok, int64_t d, int v_dtype,
                  int w_dtype, float eps, void* stream);
 
+/* Largest dw partial-row buffer sy_bwd_static can use (bytes). */
+#define SY_STATIC_WORKSPACE_BYTES (8 << 20)
+
+/* sy_bwd that allocates nothing and takes no workspace: the dw partial rows
+ * live in a static device array of SY_STATIC_WORKSPACE_BYTES per GPU (held
+ * until the process ends), resolved once per device on the first call there.
+ * No counterpart in the reference; for callers that cannot allocate device
+ * memory -- code under HIP graph capture, tight serving loops, harnesses
+ * that forbid allocation. Same kernels, grid and bits as sy_bwd. Returns
+ * SY_ERR_WORKSPACE when sy_bwd_workspace_bytes() for the shape exceeds the
+ * array. Every call on a GPU shares that GPU's array: calls that overlap on
+ * one GPU (concurrent streams, or host threads) race and must be serialised
+ * by the caller. */
+int sy_bwd_static(const void* v, const void* w, const void* grad_out, const float* stats, void* dv,
+                  void* dw, int64_t n_src, int64_t n_tok, int64_t d, int64_t src_stride, int v_dtype,
+                  int w_dtype, float eps, void* stream);
+
 /* Gradient of sy_attn_with_stats: from grad_o (v dtype [n_tok][D]) and grad_m,
  * grad_l (fp32 [n_tok]) to dv and dw, with k the first row holding the max:
  *     dlogit_n = p_n (G_n + grad_l) (n != k),  dlogit_k = grad_m - sum_{n != k} p_n (G_n + grad_l),
