@@ -83,6 +83,8 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--title", default="")
     ap.add_argument("--json-out", type=pathlib.Path, default=None)
     ap.add_argument("--sweep", action="store_true")
+    ap.add_argument("--sweep-only", default=None,
+                    help="comma list of sweep names (n-sweep, t-sweep, d-sweep, batched) or N<n> shapes")
     ap.add_argument("--schedule", action="store_true")
     ap.add_argument("--model", action="store_true")
     ap.add_argument("--model-scale", default="1.3B", choices=["1.3B", "small"])
@@ -437,7 +439,7 @@ def traffic_mode(args):
 
 
 SWEEP_SHAPES = (
-    [("n-sweep", n, 1, 4096, 2048) for n in (2, 4, 9, 16)]
+    [("n-sweep", n, 1, 4096, 2048) for n in (2, 4, 8, 9, 16, 32)]
     + [("t-sweep", 9, 1, t, 2048) for t in (512, 1024, 2048, 4096, 8192, 16384)]
     + [("d-sweep", 9, 4, 4096, d) for d in (1024, 2048, 4096)]
 )
@@ -464,7 +466,10 @@ def sweep_mode(args):
     item = torch.finfo(dt).bits // 8
     gen = torch.Generator(device=dev).manual_seed(0)
     results = []
+    only = set(args.sweep_only.split(",")) if args.sweep_only else None
     for name, n, b, t, d in SWEEP_SHAPES:
+        if only is not None and name not in only and f"N{n}" not in only:
+            continue
         nt = b * t
         slab = nt * d * item
         rot = max(2, min(6, int((3 << 30) // ((2 * n + 3) * slab))))
@@ -513,6 +518,8 @@ def sweep_mode(args):
         del sets, ws
         torch.cuda.empty_cache()
     # Config 3: batched, Q=8 queries sharing one read of v.
+    if only is not None and "batched" not in only:
+        return
     n, b, t, d, q = 9, 1, 4096, 2048, 8
     nt = b * t
     sets = [dict(v=torch.randn(n, b, t, d, device=dev, generator=gen).to(dt),

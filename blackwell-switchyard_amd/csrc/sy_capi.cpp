@@ -77,6 +77,20 @@ int bwd_grid(const sy_plan& p, int64_t n_tok, int dtype, bool stats, int variant
   return SY_OK;
 }
 
+// The backward's plan for a launch: the shape's plan with the token-count
+// rule and any override applied; a 32-row tile (which exists for the stacked
+// operator gradient with stats only) becomes the generic kernel for every
+// other caller.
+int bwd_plan(int64_t n_src, int64_t n_tok, int64_t d, int v_dtype, int w_dtype, int aligned,
+             bool stats, int variant, sy_plan* p) {
+  int rc = make_plan(SY_OP_BWD, n_src, 0, d, v_dtype, w_dtype, aligned, p, stats);
+  if (rc != SY_OK) return rc;
+  apply_tile_rules(SY_OP_BWD, n_src, n_tok, d, p);
+  if (p->family != SY_FAMILY_GENERIC && p->rows_per_tile > 16 && (!stats || variant != 0))
+    rc = make_plan(SY_OP_BWD, n_src, 0, d, v_dtype, w_dtype, 0, p, stats);
+  return rc;
+}
+
 // Partial rows the backward's workspace provides: the largest persistent
 // grid of the vector plans (every variant, with and without forward stats).
 // A call whose buffers are not 16-byte aligned runs the generic kernel, which
@@ -86,16 +100,23 @@ int bwd_grid(const sy_plan& p, int64_t n_tok, int dtype, bool stats, int variant
 int workspace_rows(int64_t n_src, int64_t n_tok, int64_t d, int v_dtype, int w_dtype, int* rows) {
   int g = 0;
   for (bool st : {true, false}) {
-    sy_plan p;
-    int rc = make_plan(SY_OP_BWD, n_src, 0, d, v_dtype, w_dtype, 1, &p, st);
-    if (rc != SY_OK) return rc;
-    apply_tile_rules(SY_OP_BWD, n_src, n_tok, d, &p);
     for (int var : {0, 1, 2}) {
+      sy_plan p;
+      int rc = bwd_plan(n_src, n_tok, d, v_dtype, w_dtype, 1, st, var, &p);
+      if (rc != SY_OK) return rc;
+      if (p.family == SY_FAMILY_GENERIC) continue;  // persistent at any grid: capped below
       int gi = 0;
       rc = bwd_grid(p, n_tok, v_dtype, st, var, &gi);
       if (rc != SY_OK) return rc;
       if (gi > g) g = gi;
     }
+  }
+  if (g == 0) {  // no vector plan at all: the generic kernel's own grid
+    sy_plan p;
+    int rc = make_plan(SY_OP_BWD, n_src, 0, d, v_dtype, w_dtype, 0, &p, true);
+    if (rc != SY_OK) return rc;
+    rc = bwd_grid(p, n_tok, v_dtype, true, 0, &g);
+    if (rc != SY_OK) return rc;
   }
   *rows = g;
   return SY_OK;
@@ -322,11 +343,10 @@ int bwd_main_impl(const RowTable& v, bool v_ok, const void* w, const void* g, co
   if (n_tok == 0) return SY_OK;
   const bool aligned = vec_rows(v_ok && dv_ok, d, v_dtype) && al16(w) && al16(g) && al16(workspace);
   sy_plan p;
-  int rc = make_plan(SY_OP_BWD, n_src, 0, d, v_dtype, w_dtype, aligned, &p, stats != nullptr);
-  if (rc != SY_OK) return rc;
-  apply_tile_rules(SY_OP_BWD, n_src, n_tok, d, &p);
-  int grid = 0;
   const int variant = listed ? 1 : (gm != nullptr ? 2 : 0);
+  int rc = bwd_plan(n_src, n_tok, d, v_dtype, w_dtype, aligned, stats != nullptr, variant, &p);
+  if (rc != SY_OK) return rc;
+  int grid = 0;
   rc = bwd_grid_for(p, n_src, n_tok, d, v_dtype, w_dtype, stats != nullptr, variant, &grid);
   if (rc != SY_OK) return rc;
   if (workspace == nullptr || workspace_bytes < (int64_t)grid * d * (int64_t)sizeof(float))
@@ -589,9 +609,8 @@ int64_t sy_bwd_partial_rows(int64_t n_src, int64_t n_tok, int64_t d, int v_dtype
   if (rc != SY_OK) return rc;
   if (n_tok == 0) return 0;
   sy_plan p;
-  rc = make_plan(SY_OP_BWD, n_src, 0, d, v_dtype, w_dtype, aligned, &p, has_stats != 0);
+  rc = bwd_plan(n_src, n_tok, d, v_dtype, w_dtype, aligned, has_stats != 0, 0, &p);
   if (rc != SY_OK) return rc;
-  apply_tile_rules(SY_OP_BWD, n_src, n_tok, d, &p);
   int grid = 0;
   rc = bwd_grid_for(p, n_src, n_tok, d, v_dtype, w_dtype, has_stats != 0, 0, &grid);
   return rc != SY_OK ? rc : grid;

@@ -29,11 +29,11 @@ struct FwdGeom {
   static constexpr int kTpb = kBlock / (64 * W);
 };
 
-// Backward: persistent workgroups of bwd_block(W, VPL) threads; kTpb token
-// slots run side by side.
-template <int W, int VPL>
+// Backward: persistent workgroups of bwd_block(W, VPL, NR) threads; kTpb
+// token slots run side by side.
+template <int W, int VPL, int NR = 0>
 struct BwdGeom {
-  static constexpr int kBlock = bwd_block(W, VPL);
+  static constexpr int kBlock = bwd_block(W, VPL, NR);
   static constexpr int kTpb = kBlock / (64 * W);
 };
 
@@ -596,7 +596,7 @@ k_sol_res(const RowTable v, typename T::storage* __restrict__ out, int n_src, in
 enum BwdVariant { kBwdStacked = 0, kBwdListed = 1, kBwdStatsGrad = 2 };
 
 template <class T, int W, int VPL, int NR, bool STATS, int VAR>
-__global__ void __launch_bounds__((BwdGeom<W, VPL>::kBlock))
+__global__ void __launch_bounds__((BwdGeom<W, VPL, NR>::kBlock))
 k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
       const typename T::storage* __restrict__ g, const float* __restrict__ stats,
       const float* __restrict__ gm, const float* __restrict__ gl, const RowTable dv,
@@ -606,7 +606,7 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
   constexpr bool GRAD_STATS = VAR == kBwdStatsGrad;
   using S = typename T::storage;
   constexpr int CE = T::ce;
-  constexpr int TPB = BwdGeom<W, VPL>::kTpb;
+  constexpr int TPB = BwdGeom<W, VPL, NR>::kTpb;
   constexpr uint32_t kStep = 64u * W * 16u;
   constexpr int kLaneFloats = VPL * CE;  // dw values a lane accumulates
   constexpr int G = STATS ? 1 : 3;       // per-row scalars reduced over D
@@ -666,12 +666,18 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
 #pragma unroll
     for (int j = 0; j < VPL; ++j) gq[j] = ld16_stream(gr, lane_off + j * kStep);
   }
-  static_assert(NR <= 16, "token scalars are spread over lanes 0..33");
+  // Lanes per statistic: 16 (lanes 32 and 33 then carry gm, gl), or 32 for
+  // the 32-row tile, whose stats fill the wave (logits in lanes 0..31, r in
+  // 32..63) and which exists only for the operator's gradient with stats.
+  constexpr int kSL = NR <= 16 ? 16 : 32;
+  static_assert(NR <= 32, "token scalars are spread over the lanes of one wave");
+  static_assert(NR <= 16 || (STATS && !GRAD_STATS && !LISTED),
+                "the 32-row tile serves the stacked operator gradient with stats only");
   // The token scalars of token t for this lane (see above); 0 for idle lanes.
   auto scalars_of = [&](int64_t t) -> float {
-    const int i = lane & 15;
+    const int i = lane & (kSL - 1);
     if constexpr (STATS) {
-      if (lane < 32 && i < rows) return stats[(int64_t)((lane >> 4) * n_src + i) * n_tok + t];
+      if (lane < 2 * kSL && i < rows) return stats[(int64_t)((lane / kSL) * n_src + i) * n_tok + t];
     }
     if constexpr (GRAD_STATS) {
       if (lane == 32) return gm[t];
@@ -733,7 +739,7 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
       if (n < rows) {
         if constexpr (STATS) {
           lg[n] = scalar(n);
-          rr[n] = scalar(16 + n);
+          rr[n] = scalar(kSL + n);
         } else {
           rr[n] = rsqrtf(fmaf(part[2 * NR + n], inv_d, eps));
           lg[n] = part[NR + n] * rr[n];
@@ -840,6 +846,236 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
       // chunk c covers elements [c*CE, c*CE + CE): CE/4 float4 stores
+      const uint32_t base = (lane_off / 16u + j * 64u * W) * CE * 4u;
+#pragma unroll
+      for (int q4 = 0; q4 < CE / 4; ++q4) {
+        i32x4_t t;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[e] = __float_as_int(dwa[j][q4 * 4 + e]);
+        st16(pr, base + q4 * 16u, t);
+      }
+    }
+  }
+}
+
+
+// ------------------------------------------------ backward, 17 to 32 sources
+//
+// The operator's gradient with the forward's stats over stacked rows for
+// 16 < N <= 32: k_bwd's algebra, persistence and row-by-row refill, with the
+// token's per-row scalars laid out across lanes instead of held as uniform
+// values: lane n of one VGPR each carries row n's G_n, logit, r, alpha, da
+// and c. The softmax backward is then a few lane-parallel operations and
+// three wave reductions, where 32 rows of uniform scalar code (as k_bwd
+// writes it) needed ~300 SGPRs and spilled them into VGPR lanes on every
+// token. The dv loop broadcasts row n's three coefficients with readlane as
+// it reaches the row. Rows n >= N are never loaded; their lanes carry
+// logit -inf (weight 0) and zero coefficients.
+// x, hidden from the optimiser: a comparison against it cannot be hoisted and
+// kept live (32 row guards kept as 64-bit predicates spilled SGPRs).
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+s"(x));
+  return x;
+}
+
+template <int W, int VPL>
+struct TallGeom {
+  static constexpr int kBlock = bwd_block(W, VPL, 32);
+  static constexpr int kTpb = kBlock / (64 * W);
+};
+
+template <class T, int W, int VPL>
+__global__ void __launch_bounds__((TallGeom<W, VPL>::kBlock))
+k_bwd_tall(const RowTable v, const typename T::storage* __restrict__ w,
+           const typename T::storage* __restrict__ g, const float* __restrict__ stats,
+           const RowTable dv, float* __restrict__ partial, int n_src, int64_t n_tok, int d,
+           float inv_d, int n_iter) {
+  using S = typename T::storage;
+  constexpr int CE = T::ce;
+  constexpr int NR = 32;
+  constexpr int TPB = TallGeom<W, VPL>::kTpb;
+  constexpr uint32_t kStep = 64u * W * 16u;
+  constexpr int kLaneFloats = VPL * CE;
+  constexpr int kFH = TPB > 1 ? TPB / 2 : 1;
+  constexpr int kFW = TPB > 1 ? W : 1;
+  constexpr int kFL = TPB > 1 ? 64 : 1;
+  static_assert(W > 1, "a 32-row token spans at least two waves");
+  __shared__ float red[2][TPB][W][NR];
+  __shared__ float fold[kFH][kFW][kFL][kLaneFloats + 1];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int slot = wave / W;
+  const int seg = wave % W;
+  const uint32_t row_bytes = (uint32_t)d * sizeof(S);
+  const uint32_t lane_off = (uint32_t)(seg * 64 + lane) * 16u;
+  const int64_t slots = (int64_t)gridDim.x * TPB;
+  const int64_t first = (int64_t)blockIdx.x * TPB + slot;
+  const int rows = n_src;  // host guarantees 16 < n_src <= 32
+  const bool row_lane = lane < rows;
+  const int iters = n_iter;  // every slot meets the same barriers
+
+  float wf[VPL][CE];
+  i32x4_t wq[VPL];
+  {
+    const auto wr = make_rsrc(w, row_bytes);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      wq[j] = ld16(wr, lane_off + j * kStep);
+#pragma unroll
+      for (int e = 0; e < CE; ++e) wf[j][e] = elem<T>(wq[j], e);
+    }
+  }
+  float dwa[VPL][CE];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j)
+#pragma unroll
+    for (int e = 0; e < CE; ++e) dwa[j][e] = 0.0f;
+
+  i32x4_t x[NR][VPL];
+  i32x4_t gq[VPL];
+  const int64_t t0 = first < n_tok ? first : n_tok - 1;
+  {
+    const S* vrow = static_cast<const S*>(v.p[0]) + t0 * d;
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      if (n < opaque(rows)) {
+        asm volatile("" : "+s"(vrow));
+        const auto r = make_rsrc(vrow, row_bytes);
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
+        vrow = reinterpret_cast<const S*>(reinterpret_cast<const char*>(vrow) + v.stride_bytes);
+      }
+    }
+    const auto gr = make_rsrc(g + t0 * d, row_bytes);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) gq[j] = ld16_stream(gr, lane_off + j * kStep);
+  }
+  // Row `lane`'s logit and inverse RMS of token t, one token ahead.
+  auto logit_of = [&](int64_t t) { return row_lane ? stats[(int64_t)lane * n_tok + t] : -INFINITY; };
+  auto rinv_of = [&](int64_t t) { return row_lane ? stats[(int64_t)(n_src + lane) * n_tok + t] : 0.0f; };
+  float lg_next = logit_of(t0), r_next = rinv_of(t0);
+
+  for (int k = 0; k < iters; ++k) {
+    const int64_t tok_raw = first + (int64_t)k * slots;
+    const bool live = tok_raw < n_tok;
+    const int64_t tok = live ? tok_raw : n_tok - 1;
+    const bool more = k + 1 < iters;
+    const int64_t nxt = tok_raw + slots < n_tok ? tok_raw + slots : n_tok - 1;
+    const float lg = lg_next, rr = r_next;
+    if (more) {
+      lg_next = logit_of(nxt);
+      r_next = rinv_of(nxt);
+    }
+
+    // G_n = <g, v_n>: this wave's share into lane n, then the W shares of the
+    // token added in segment order through LDS.
+    float gv = 0.0f;
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      if (n < opaque(rows)) {
+        float dt = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) dt = dot<T>(x[n][j], gq[j], dt);
+        const float s = wave_sum(dt);
+        gv = lane == n ? s : gv;
+      }
+    }
+    if (lane < NR) red[k & 1][slot][seg][lane] = gv;
+    __syncthreads();
+    if (lane < NR) {
+      float t = red[k & 1][slot][0][lane];
+#pragma unroll
+      for (int q = 1; q < W; ++q) t += red[k & 1][slot][q][lane];
+      gv = t;
+    }
+
+    // Softmax backward across lanes, relative to the first row with the
+    // largest logit (cancellation-free, as in k_bwd).
+    const float m = wave_max(lg);
+    const int top = (int)__builtin_ctzll(__builtin_amdgcn_ballot_w64(lg == m));
+    const float gref = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gv), top));
+    float al = row_lane ? expf(lg - m) : 0.0f;
+    al *= 1.0f / wave_sum(al);
+    const float dd = row_lane ? gv - gref : 0.0f;
+    const float sdev = wave_sum(al * dd);
+    const float dlogit = al * (dd - sdev);
+    const float da = dlogit * rr;
+    const float c = -dlogit * (row_lane ? lg : 0.0f) * rr * rr * inv_d;
+
+    float gf[VPL][CE];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+#pragma unroll
+      for (int e = 0; e < CE; ++e) gf[j][e] = elem<T>(gq[j], e);
+    if (more) {
+      const auto gr = make_rsrc(g + nxt * d, row_bytes);
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) gq[j] = ld16_stream(gr, lane_off + j * kStep);
+    }
+    const float dw_on = live ? 1.0f : 0.0f;
+    float alv = al, dav = da, cv = c;
+    // Row n's addresses walk from row 0 one stride at a time; the empty asm
+    // keeps the walk serial, so the 2 x 32 row addresses (and their buffer
+    // resources) are never all live at once in SGPRs.
+    const S* vrow = static_cast<const S*>(v.p[0]) + nxt * d;
+    S* dvrow = static_cast<S*>(dv.p[0]) + tok * d;
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      if (n < opaque(rows)) {
+        // Keep the broadcasts at their row: hoisted, the 3 x 32 uniform
+        // coefficients would need SGPRs again.
+        asm volatile("" : "+v"(alv), "+v"(dav), "+v"(cv), "+s"(vrow), "+s"(dvrow));
+        const float aln = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alv), n));
+        const float dan = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dav), n));
+        const float cn = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cv), n));
+        const float da_w = dan * dw_on;
+        const auto dr = make_rsrc(dvrow, live ? row_bytes : 0u);
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+          float f[CE];
+#pragma unroll
+          for (int e = 0; e < CE; ++e) {
+            const float xv = elem<T>(x[n][j], e);
+            f[e] = fmaf(cn, xv, fmaf(dan, wf[j][e], aln * gf[j][e]));
+            dwa[j][e] = fmaf(da_w, xv, dwa[j][e]);
+          }
+          st16_stream(dr, lane_off + j * kStep, pack<T>(f));
+        }
+        if (more) {
+          const auto r = make_rsrc(vrow, row_bytes);
+#pragma unroll
+          for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
+        }
+        vrow = reinterpret_cast<const S*>(reinterpret_cast<const char*>(vrow) + v.stride_bytes);
+        dvrow = reinterpret_cast<S*>(reinterpret_cast<char*>(dvrow) + dv.stride_bytes);
+      }
+    }
+  }
+
+  // Fold the TPB slot accumulators (slots [h, 2h) into [0, h)), then one fp32
+  // partial row per workgroup.
+#pragma unroll
+  for (int h = TPB / 2; h >= 1; h /= 2) {
+    __syncthreads();
+    if (slot >= h && slot < 2 * h) {
+#pragma unroll
+      for (int j = 0; j < VPL; ++j)
+#pragma unroll
+        for (int e = 0; e < CE; ++e) fold[slot - h][seg][lane][j * CE + e] = dwa[j][e];
+    }
+    __syncthreads();
+    if (slot < h) {
+#pragma unroll
+      for (int j = 0; j < VPL; ++j)
+#pragma unroll
+        for (int e = 0; e < CE; ++e) dwa[j][e] += fold[slot][seg][lane][j * CE + e];
+    }
+  }
+  if (slot == 0) {
+    const auto pr = make_rsrc(partial + (int64_t)blockIdx.x * d, (uint32_t)d * 4u);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
       const uint32_t base = (lane_off / 16u + j * 64u * W) * CE * 4u;
 #pragma unroll
       for (int q4 = 0; q4 < CE / 4; ++q4) {

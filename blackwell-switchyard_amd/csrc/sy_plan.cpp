@@ -22,6 +22,8 @@
 //     admits 16 rows x 2 chunks when the forward's stats are passed (that
 //     variant holds no recompute state and fits 256 VGPRs); without stats that
 //     tile spills and the thinner one is kept.
+//     16 < N <= 32 with stats: the 32-row tile, one chunk per lane on the 2 or
+//     4 waves that cover the row, or two chunks on 4 (D = 4096 in bf16).
 //  5. Batched: 16-bit inputs with N <= 16, 6 <= S <= 16 and D in {512, 1024,
 //     1536, 2048} run on the matrix cores (config 3: 8 queries x 9 rows is ~7000
 //     VALU instructions a token on the register tile); otherwise resident with
@@ -72,7 +74,7 @@ void set(sy_plan* p, int family, int w, int vpl, int nr, int ce, int op, int64_t
     return;
   }
   if (op == SY_OP_BWD) {
-    p->block_threads = bwd_block(w, vpl);
+    p->block_threads = bwd_block(w, vpl, nr);
     p->tokens_per_block = p->block_threads / (64 * w);
   } else {
     p->block_threads = 64 * w > 256 ? 64 * w : 256;
@@ -157,6 +159,17 @@ int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_
   // would share a SIMD and spill. The 16-row tile holds 256 VGPRs of source
   // rows: its recompute variant (no stats) spills 68 bytes a lane and still
   // beats the thinner tiles (N=16: 119 vs 167 us).
+  // 16 < N <= 32 with the forward's stats: 32 rows resident at one wave per
+  // SIMD, one chunk per lane on two or four waves, or two chunks on four
+  // (v read once; the generic kernel reads it twice with element-wise loads).
+  // Without stats the per-row scalars would not fit; that case stays generic.
+  if (vec && op == SY_OP_BWD && has_stats && n_src > 16 && n_src <= kTallRows && e > 64) {
+    const int ww = e <= 128 ? 2 : 4, vv = e <= 256 ? 1 : 2;
+    if (e <= 512) {
+      set(out, SY_FAMILY_RESIDENT, ww, vv, kTallRows, ce, op, n_src);
+      return SY_OK;
+    }
+  }
   if (vec && op == SY_OP_BWD && n_src > 4 && n_src <= 16) {
     for (int ww : {1, 2, 4}) {
       if (n_src > 9 && ww == 4) break;
@@ -215,6 +228,7 @@ bool tile_listed(int op, int w, int vpl, int nr) {
   SY_TILES(X)
   if (op == SY_OP_BWD) {
     SY_BWD_WIDE_TILES(X)
+    SY_BWD_TALL_TILES(X)
   }
 #undef X
   return false;

@@ -207,11 +207,21 @@ def test_tiles_cover_the_row_exactly_once():
                             assert p["rows_per_tile"] >= n
 
 
-def test_large_n_forward_uses_online_chunks_and_backward_the_generic_kernel():
+def test_large_n_forward_uses_online_chunks_and_backward_the_32_row_tile():
     f = plan(_lib.OP_FWD, 33, 512)
     assert f["family_name"] == "chunked" and f["n_chunks"] == 3
     assert plan(_lib.OP_FWD, 17, 2048)["family_name"] == "chunked"
-    assert plan(_lib.OP_BWD, 17, 2048)["family_name"] == "generic"
+    # 16 < N <= 32 (with the forward's stats): 32 rows resident
+    for n, d, dt, tile in ((17, 2048, torch.bfloat16, (4, 1, 32)), (32, 2048, torch.bfloat16, (4, 1, 32)),
+                           (24, 1024, torch.float16, (2, 1, 32)), (32, 4096, torch.bfloat16, (4, 2, 32)),
+                           (32, 2048, torch.float32, (4, 2, 32))):
+        p = plan(_lib.OP_BWD, n, d, dt)
+        assert p["family_name"] == "resident", (n, d)
+        assert (p["waves_per_token"], p["chunks_per_lane"], p["rows_per_tile"]) == tile
+        assert p["block_threads"] == (512 if tile[1] == 1 else 256)  # two waves per SIMD, or one
+    # beyond 32 rows, above 4096 bf16 columns or below 128: generic
+    for n, d in ((33, 2048), (32, 8192), (20, 512)):
+        assert plan(_lib.OP_BWD, n, d)["family_name"] == "generic", (n, d)
 
 
 def test_unaligned_rows_and_mixed_dtypes_take_the_generic_kernels():

@@ -85,15 +85,18 @@ def test_hip_mechanism_tracks_the_framework_through_an_adamw_step():
     fw = _step("attnres")
     hip = _step("switchyard")
     print(f"  fp32 attnres {ref32}\n  bf16 attnres {fw}\n  bf16 switchyard {hip}", flush=True)
+    # Observed on MI355X: losses within 1.3e-4 (relative) of each other and
+    # 4e-4 of fp32; group norms within 1.5e-3 of each other and 1.8e-3 of
+    # fp32. The bars leave several times that.
     for key in ("loss", "after"):
-        assert abs(hip[key] - fw[key]) <= 2e-3 * abs(fw[key]), key
+        assert abs(hip[key] - fw[key]) <= 1e-3 * abs(fw[key]), key
         # no further from the fp32 evaluation than the framework's bf16 is
         assert abs(hip[key] - ref32[key]) <= 2.0 * abs(fw[key] - ref32[key]) + 1e-3 * abs(ref32[key]), key
     assert set(hip["norms"]) == set(fw["norms"])
     for grp, ref in fw["norms"].items():
         got, truth = hip["norms"][grp], ref32["norms"][grp]
-        assert abs(got - ref) <= 5e-2 * ref, (grp, got, ref)
-        assert abs(got - truth) <= 2.0 * abs(ref - truth) + 2e-2 * truth, (grp, got, ref, truth)
+        assert abs(got - ref) <= 1e-2 * ref, (grp, got, ref)
+        assert abs(got - truth) <= 2.0 * abs(ref - truth) + 5e-3 * truth, (grp, got, ref, truth)
 
 
 def test_source_modes_give_bit_identical_logits():

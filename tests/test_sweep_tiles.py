@@ -70,6 +70,11 @@ SWEEP_CASES = [
     # token count being above two per CU)
     ((9, 4, 256, 1024), ("resident", (1, 2, 9)), (1, 2, 9)),
     ((9, 4, 256, 4096), ("resident", (2, 4, 9)), (2, 4, 9)),
+    # 16 < N <= 32: the 32-row backward tile (the reference's n-sweep has N=32)
+    ((32, 1, 4096, 2048), ("chunked", (1, 4, 4)), (4, 1, 32)),
+    ((17, 1, 4 * 256, 2048), ("chunked", (1, 4, 4)), (4, 1, 32)),
+    ((24, 4, 256, 1024), ("chunked", (1, 2, 16)), (2, 1, 32)),
+    ((32, 1, 1024, 4096), ("chunked", (2, 4, 4)), (4, 2, 32)),
 ]
 
 
@@ -77,7 +82,7 @@ SWEEP_CASES = [
 @pytest.mark.parametrize("shape,fwd,bwd", SWEEP_CASES, ids=[f"N{s[0]}B{s[1]}T{s[2]}D{s[3]}" for s, _, _ in SWEEP_CASES])
 def test_sweep_shape_runs_its_tile_at_the_oracle_floor(shape, fwd, bwd, dtype):
     n, b, t, d = shape
-    if shape == (12, 1, 4 * 256, 2048):
+    if shape in ((12, 1, 4 * 256, 2048), (17, 1, 4 * 256, 2048)):
         t = 4 * CUS  # four tokens per CU on any device
     n_tok = b * t
     assert n_tok > 2 * CUS, "the token-count rule would pick another tile"
@@ -86,3 +91,57 @@ def test_sweep_shape_runs_its_tile_at_the_oracle_floor(shape, fwd, bwd, dtype):
     assert _tile(_lib.OP_BWD, n, d, dtype, n_tok) == ("resident", bwd)
     res = _check(n, b, t, d, dtype, seed=100 + n + d // 512)
     print(f"  ratios to the floor: {res}", flush=True)
+
+
+@pytest.mark.parametrize("n,t,d", [(32, 1024, 2048), (19, 600, 1024)])
+def test_32_row_tile_in_fp32(n, t, d):
+    """fp32 rows take the two-chunk 32-row tile at D=2048 (512 chunks) and the
+    one-chunk tile at D=1024; bar: the reference's fp32 tolerance."""
+    tile = (4, 2, 32) if d == 2048 else (4, 1, 32)
+    assert _tile(_lib.OP_BWD, n, d, torch.float32, t) == ("resident", tile)
+    gen = torch.Generator().manual_seed(n)
+    v = torch.randn(n, 1, t, d, generator=gen)
+    w = 0.5 * torch.randn(d, generator=gen)
+    g = torch.randn(1, t, d, generator=gen)
+    vv, ww = v.to(DEV).requires_grad_(True), w.to(DEV).requires_grad_(True)
+    out = block_attn_res_hip(vv, ww)
+    out.backward(g.to(DEV))
+    v64 = v.double()[:, 0].numpy()
+    ro = torch.from_numpy(c_oracle.forward(v64, w.double().numpy()))
+    rdv, rdw = c_oracle.backward(v64, w.double().numpy(), g.double()[0].numpy())
+    assert rel_l2(out.detach()[0].cpu(), ro) <= 1e-6
+    assert rel_l2(vv.grad[:, 0].cpu(), torch.from_numpy(rdv)) <= 1e-5
+    assert rel_l2(ww.grad.cpu(), torch.from_numpy(rdw)) <= 1e-5
+
+
+def test_32_row_tile_is_bitwise_deterministic_and_other_callers_fall_back():
+    """Two runs give the same bits; without the forward's stats the backward
+    at N > 16 runs the generic kernel and still matches."""
+    import ctypes
+
+    n, t, d = 24, 3 * CUS, 2048
+    gen = torch.Generator().manual_seed(3)
+    v = torch.randn(n, 1, t, d, generator=gen).to(torch.bfloat16).to(DEV)
+    w = (0.5 * torch.randn(d, generator=gen)).to(torch.bfloat16).to(DEV)
+    g = torch.randn(1, t, d, generator=gen).to(torch.bfloat16).to(DEV)
+    grads = []
+    for _ in range(2):
+        vv, ww = v.clone().requires_grad_(True), w.clone().requires_grad_(True)
+        block_attn_res_hip(vv, ww).backward(g)
+        grads.append((vv.grad, ww.grad))
+    assert torch.equal(grads[0][0], grads[1][0]) and torch.equal(grads[0][1], grads[1][1])
+    lib, code = _lib.lib(), _lib.dtype_code(torch.bfloat16)
+    ws_bytes = lib.sy_bwd_workspace_bytes(n, t, d, code, code)
+    ws = torch.empty(ws_bytes // 4, device=DEV)
+    dv, dw = torch.empty_like(v), torch.empty(d, device=DEV, dtype=torch.bfloat16)
+    P = ctypes.c_void_p
+    rc = lib.sy_bwd(P(v.data_ptr()), P(w.data_ptr()), P(g.data_ptr()), None, P(dv.data_ptr()), P(dw.data_ptr()),
+                    P(ws.data_ptr()), ws_bytes, n, t, d, t * d, code, code, 1e-6, _lib.stream_ptr(v.device))
+    assert rc == 0
+    torch.cuda.synchronize()
+    for got, ref in ((dv, grads[0][0]), (dw, grads[0][1])):
+        assert rel_l2(got.cpu(), ref.cpu()) <= 1e-2  # two bf16 roundings of the same values
+    v64 = v.double()[:, 0].cpu().numpy()
+    rdv, rdw = c_oracle.backward(v64, w.double().cpu().numpy(), g.double()[0].cpu().numpy())
+    for got, ref in ((dv[:, 0], torch.from_numpy(rdv)), (dw, torch.from_numpy(rdw))):
+        assert rel_l2(got.cpu(), ref) <= 1.10 * dtype_floor(ref, torch.bfloat16)
