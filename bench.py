@@ -82,6 +82,11 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--summarize", type=pathlib.Path, default=None)
     ap.add_argument("--title", default="")
     ap.add_argument("--json-out", type=pathlib.Path, default=None)
+    ap.add_argument("--quick", action="store_true",
+                    help="--schedule / --sweep: a few launches per row and a copy-probe calibration "
+                         "launch at the end (a rocprofv3 --pmc target)")
+    ap.add_argument("--traffic-set", default="config2", choices=["config2", "schedule", "n32"],
+                    help="--traffic: which kernels and workload the counter runs covered")
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--sweep-only", default=None,
                     help="comma list of sweep names (n-sweep, t-sweep, d-sweep, batched) or N<n> shapes")
@@ -403,6 +408,45 @@ def _counter_means(d: pathlib.Path, counter: str) -> dict[str, float]:
     return {k: sum(v) / len(v) for k, v in agg.items()}
 
 
+def _copy_probe_calibration(torch, dev) -> None:
+    """Three launches of the 1 GiB copy probe: the known-size kernel that
+    calibrates FETCH_SIZE and WRITE_SIZE in a counter run."""
+    from switchyard.hip_op import bandwidth_probe
+
+    nbytes = 1 << 30
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(3)
+    dst = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    for _ in range(3):
+        bandwidth_probe("copy", src, dst)
+    torch.cuda.synchronize(dev)
+
+
+def _traffic_kernels(args):
+    """(label, name substring, excluded substring, algorithmic bytes per launch,
+    workload) of the kernels a counter run of --traffic-set covered."""
+    slab = args.b * args.t * args.d * 2
+    if args.traffic_set == "config2":
+        n = args.n
+        wl = f"N={n} B={args.b} T={args.t} D={args.d} bf16"
+        return [("fwd", "k_fwd_res", None, (n + 1) * slab, wl),
+                ("bwd_main", "k_bwd<", None, (2 * n + 1) * slab, wl),
+                ("sol", "k_sol_res", None, (n + 1) * slab, wl)]
+    if args.traffic_set == "schedule":  # bench.py --schedule --quick
+        n, s, d = 9, 8, 2048
+        slab = 4096 * d * 2
+        wl = f"N={n} B=1 T=4096 D={d} bf16, S={s} queries"
+        return [("batched_fwd", "k_batched_mx", None, (n + s) * slab + s * d * 2, wl),
+                ("batched_bwd", "k_bwd_batched_mx", None, (2 * n + s) * slab + s * d * 2, wl),
+                ("merge_fwd", "k_merge", "k_merge_bwd", 3 * slab + 6 * 4096 * 4, wl),
+                ("merge_bwd", "k_merge_bwd", None, 5 * slab + 10 * 4096 * 4, wl),
+                ("table_bwd", "true, 1>", None, (2 * n + 1) * slab, wl)]
+    n, d = 32, 2048  # bench.py --sweep --sweep-only N32 --quick
+    slab = 4096 * d * 2
+    wl = f"N={n} B=1 T=4096 D={d} bf16"
+    return [("fwd_chunked", "k_fwd<", None, (n + 1) * slab, wl),
+            ("bwd_tall", "k_bwd_tall", None, (2 * n + 1) * slab, wl)]
+
+
 def traffic_mode(args):
     """HBM bytes per launch from FETCH_SIZE / WRITE_SIZE (KiB per dispatch),
     each scaled so the 1 GiB copy probe reads and writes exactly 1 GiB."""
@@ -418,15 +462,19 @@ def traffic_mode(args):
     gib_kib = float(1 << 20)
     fscale = gib_kib / pick(fetch, "k_probe_copy")
     wscale = gib_kib / pick(write, "k_probe_copy")
-    slab = args.b * args.t * args.d * 2
-    algo = {"k_fwd_res": (args.n + 1) * slab, "k_bwd<": (2 * args.n + 1) * slab, "k_sol_res": (args.n + 1) * slab}
-    rec = {"workload": f"N={args.n} B={args.b} T={args.t} D={args.d} bf16", "fetch_scale": fscale,
-           "write_scale": wscale, "method": "rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE (KiB per dispatch), "
-           "each scaled by what the counter reads for the 1 GiB copy probe"}
-    for needle, nbytes in algo.items():
-        f_kib, w_kib = pick(fetch, needle), pick(write, needle)
+    kernels = _traffic_kernels(args)
+    rec = {"workload": kernels[0][4], "fetch_scale": fscale, "write_scale": wscale,
+           "method": "rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE (KiB per dispatch), each scaled by what the "
+                     "counter reads for the 1 GiB copy probe"}
+    for key, needle, exclude, nbytes, _ in kernels:
+        def hit(table):
+            vals = [v for k, v in table.items() if needle in k and (exclude is None or exclude not in k)]
+            if not vals:
+                raise SystemExit(f"no dispatch of {needle} in the counter data")
+            return sum(vals) / len(vals)
+
+        f_kib, w_kib = hit(fetch), hit(write)
         tot = (f_kib * fscale + w_kib * wscale) * 1024
-        key = {"k_fwd_res": "fwd", "k_bwd<": "bwd_main", "k_sol_res": "sol"}[needle]
         rec[f"{key}_bytes_per_launch"] = round(tot)
         rec[f"{key}_fetch_kib"] = f_kib
         rec[f"{key}_write_kib"] = w_kib
@@ -496,8 +544,11 @@ def sweep_mode(args):
         for s in sets:  # warm-up: a shape's first launches query kernel attributes
             fwd(s)
             bwd(s)
-        f_ms = harness.time_loop_median([lambda s=s: fwd(s) for s in sets], device=dev, iters=iters)
-        fb_ms = harness.time_loop_median([lambda s=s: (fwd(s), bwd(s)) for s in sets], device=dev, iters=iters)
+        loop = harness.time_loop if args.quick else harness.time_loop_median
+        if args.quick:
+            iters = 3
+        f_ms = loop([lambda s=s: fwd(s) for s in sets], device=dev, iters=iters)
+        fb_ms = loop([lambda s=s: (fwd(s), bwd(s)) for s in sets], device=dev, iters=iters)
         fb = attn_res_train_bytes(n, b, t, d, item)
         fw = attn_res_min_bytes(n, b, t, d, item)
         fplan = _lib.plan(_lib.OP_FWD, n, d, dt, n_tok=nt)
@@ -519,6 +570,8 @@ def sweep_mode(args):
         torch.cuda.empty_cache()
     # Config 3: batched, Q=8 queries sharing one read of v.
     if only is not None and "batched" not in only:
+        if args.quick:
+            _copy_probe_calibration(torch, dev)
         return
     n, b, t, d, q = 9, 1, 4096, 2048, 8
     nt = b * t
@@ -578,6 +631,8 @@ def schedule_mode(args):
     def timed(fns, iters=100):
         for f in fns:
             f()
+        if args.quick:
+            return harness.time_loop(fns, device=dev, iters=3)
         return harness.time_loop_median(fns, device=dev, iters=iters)
 
     # --- pointer table vs stacked (config 2) ---------------------------------
@@ -691,6 +746,8 @@ def schedule_mode(args):
          Q=nq, workspace_bytes=bw_bytes,
          note="reads v and the Q output gradients once, writes dv once; S separate backward calls would move "
               f"{nq * (2 * n + 1)} slabs instead of {2 * n + nq}")
+    if args.quick:
+        _copy_probe_calibration(torch, dev)
     if args.json_out:
         args.json_out.parent.mkdir(parents=True, exist_ok=True)
         args.json_out.write_text(json.dumps({"environment": harness.environment(), "results": results}, indent=1))
