@@ -759,6 +759,56 @@ MODEL_SCALES = {
 }
 
 
+def profile_step(model, step, dev, iters: int = 3) -> dict:
+    """Device time of the residual mechanism inside training steps, from a
+    torch.profiler trace: the HIP operator's kernels are found by name (every
+    one lives in the ``sy::`` namespace: forward, backward, dw reduction), the
+    source staging (arena slot copies, ``torch.stack``) by its
+    ``attnres_stage`` region, and for the eager mechanism, whose kernels are
+    generic, the forward by its ``attnres_op`` region (its backward cannot be
+    told apart and is reported as None). Reference: bench/bench_model.py:211-255
+    attributes by region and autograd-node name."""
+    import torch
+    from torch.profiler import ProfilerActivity, profile
+
+    regions = ("attnres_stage", "attnres_op")
+    model.profile_regions = True
+    try:
+        for _ in range(2):
+            step()
+        torch.cuda.synchronize(dev)
+        with profile(activities=[ProfilerActivity.CPU, ProfilerActivity.CUDA]) as prof:
+            for _ in range(iters):
+                step()
+            torch.cuda.synchronize(dev)
+    finally:
+        model.profile_regions = False
+    total = op_kernels = 0.0
+    region_dev: dict[str, float] = {}
+    for e in prof.key_averages():
+        if e.device_type == torch.autograd.DeviceType.CUDA:
+            if e.key in regions or e.key.startswith(("Memcpy", "Memset")):
+                continue
+            total += e.self_device_time_total
+            if "sy::" in e.key:
+                op_kernels += e.self_device_time_total
+        elif e.key in regions:
+            region_dev[e.key] = region_dev.get(e.key, 0.0) + e.device_time_total
+    out = {"iters": iters, "total_device_us": round(total / iters, 1),
+           "staging_us": round(region_dev.get("attnres_stage", 0.0) / iters, 1)}
+    hip = model.cfg.residual == "switchyard"
+    if model.cfg.residual == "standard":
+        return out
+    if hip:
+        out["operator_kernels_us"] = round(op_kernels / iters, 1)
+        out["attnres_share_of_device_time"] = round((op_kernels / iters + out["staging_us"]) / out["total_device_us"], 4)
+    else:
+        out["operator_forward_us"] = round(region_dev.get("attnres_op", 0.0) / iters, 1)
+        out["operator_backward_us"] = None
+        out["attnres_share_of_device_time"] = None
+    return out
+
+
 def model_mode(args):
     """Config 5: tokens/s of a bf16 AdamW training step (reference bench/bench_model.py)."""
     import torch
@@ -769,14 +819,17 @@ def model_mode(args):
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     bsz, seq = args.model_batch, args.model_seq
-    variants = [("standard", "arena"), ("attnres", "arena"), ("switchyard", "arena"), ("switchyard", "stack")]
+    variants = [("standard", "arena"), ("attnres", "arena"), ("switchyard", "arena"), ("switchyard", "stack"),
+                ("switchyard", "table")]
     out = {"metric": "decoder training step tokens/s (config 5)", "scale": args.model_scale,
            "config": MODEL_SCALES[args.model_scale], "batch": bsz, "seq": seq, "dtype": "bf16",
            "data": "uniform-random token ids, random-init weights (seed 0)", "variants": []}
     for residual, sources in variants:
         torch.manual_seed(0)
         cfg = ModelConfig(**MODEL_SCALES[args.model_scale], residual=residual, sources=sources)
-        model = Transformer(cfg).to(device=dev, dtype=torch.bfloat16)
+        with dev:  # initialise on the device
+            model = Transformer(cfg)
+        model = model.to(dtype=torch.bfloat16)
         opt = torch.optim.AdamW(model.parameters(), lr=1e-6)
         idx = torch.randint(0, cfg.vocab_size, (bsz, seq), device=dev)
         tgt = torch.randint(0, cfg.vocab_size, (bsz, seq), device=dev)
@@ -800,6 +853,9 @@ def model_mode(args):
                "forward_nograd_ms": round(t_fwd.median_ms, 3),
                "tokens_per_s": round(bsz * seq / (t_step.median_ms * 1e-3), 1),
                "peak_memory_gib": round(torch.cuda.max_memory_allocated(dev) / 2**30, 2)}
+        if residual != "standard":
+            rec["source_counts"] = sum(model.last_source_counts)
+        rec["profile"] = profile_step(model, step, dev)
         out["variants"].append(rec)
         log(json.dumps(rec))
         del model, opt
@@ -807,6 +863,16 @@ def model_mode(args):
     base = out["variants"][0]["step_ms"]
     for r in out["variants"][1:]:
         r["share_of_step_vs_control"] = round(1 - base / r["step_ms"], 4)
+        prof = r.get("profile", {})
+        base_dev = out["variants"][0].get("profile", {}).get("total_device_us")
+        if base_dev and prof.get("total_device_us"):
+            # device-time difference against the control, as a share of this
+            # variant's device time: what the mechanism adds on the GPU
+            r["device_share_vs_control"] = round(1 - base_dev / prof["total_device_us"], 4)
+        if prof.get("attnres_share_of_device_time") is not None:
+            # The two measures of the mechanism's cost should agree: the
+            # control difference (whole steps) and the profiler's device time.
+            r["share_agreement"] = round(prof["attnres_share_of_device_time"] - r["share_of_step_vs_control"], 4)
     out["reference_rtx_pro_6000"] = {"standard_tok_s": 19101, "switchyard_arena_tok_s": 16918,
                                      "note": "reference README.md:82-84, vocab 32768"}
     print(json.dumps(out), flush=True)

@@ -803,11 +803,12 @@ int64_t sy_probe_grid(int64_t bytes) {
 }
 
 int sy_bw_probe(int kind, const void* src, void* dst, int64_t bytes, void* stream) {
-  if (kind < 0 || kind > 2) return SY_ERR_OP;
-  if (bytes <= 0 || bytes % 16 != 0) return SY_ERR_SHAPE;
+  if (kind < 0 || kind > 3) return SY_ERR_OP;
+  if (bytes <= 0 || bytes % 16 != 0 || (kind == 3 && bytes % 144 != 0)) return SY_ERR_SHAPE;
   if ((kind != 1 && src == nullptr) || dst == nullptr) return SY_ERR_NULL;
   if ((kind != 1 && !al16(src)) || (kind != 0 && !al16(dst))) return SY_ERR_SHAPE;
-  return status(launch_probe(kind, src, dst, bytes, (int)sy_probe_grid(bytes), (hipStream_t)stream));
+  const int64_t grid = kind == 3 ? sy_probe_grid(bytes / 9 * 4) : sy_probe_grid(bytes);
+  return status(launch_probe(kind, src, dst, bytes, (int)grid, (hipStream_t)stream));
 }
 
 int sy_tuning_set(const sy_tuning* t) {

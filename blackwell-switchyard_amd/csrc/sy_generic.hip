@@ -467,6 +467,28 @@ k_probe_copy(const char* __restrict__ src, char* __restrict__ dst, int64_t bytes
   }
 }
 
+// 9:1 mix probe: each workgroup step reads 36 KiB of one contiguous source
+// stretch (nine 4 KiB sub-blocks, each load instruction of a wave 1 KiB
+// contiguous, nine loads in flight per thread) and writes 4 KiB: output chunk
+// c of the step is the sum of chunk c of the nine sub-blocks. The forward's
+// bytes and read:write ratio without its 16 MiB row stride.
+__global__ void __launch_bounds__(256)
+k_probe_mix(const char* __restrict__ src, char* __restrict__ dst, int64_t out_bytes) {
+  constexpr int64_t kOut = 256 * 16;  // output bytes per workgroup step
+  for (int64_t base = (int64_t)blockIdx.x * kOut; base < out_bytes; base += (int64_t)gridDim.x * kOut) {
+    const uint32_t len = (uint32_t)(out_bytes - base < kOut ? out_bytes - base : kOut);
+    const auto r = make_rsrc(src + 9 * base, 9 * len);
+    const auto w = make_rsrc(dst + base, len);
+    i32x4_t x[9];
+#pragma unroll
+    for (int u = 0; u < 9; ++u) x[u] = ld16_stream(r, (u * 256u + threadIdx.x) * 16u);
+    i32x4_t acc = x[0];
+#pragma unroll
+    for (int u = 1; u < 9; ++u) acc += x[u];
+    st16_stream(w, threadIdx.x * 16u, acc);
+  }
+}
+
 }  // namespace
 
 hipError_t launch_fwd_generic(const FwdArgs& a, hipStream_t s) {
@@ -518,9 +540,12 @@ hipError_t launch_probe(int kind, const void* src, void* dst, int64_t bytes, int
                        (float*)dst);
   } else if (kind == 1) {
     hipLaunchKernelGGL(k_probe_write, dim3(grid), dim3(256), 0, s, (i32x4_t*)dst, n16);
-  } else {
+  } else if (kind == 2) {
     hipLaunchKernelGGL(k_probe_copy, dim3(grid), dim3(256), 0, s, (const char*)src, (char*)dst,
                        bytes);
+  } else {
+    hipLaunchKernelGGL(k_probe_mix, dim3(grid), dim3(256), 0, s, (const char*)src, (char*)dst,
+                       bytes / 9);
   }
   return hipGetLastError();
 }

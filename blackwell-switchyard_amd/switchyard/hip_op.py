@@ -273,8 +273,10 @@ def speed_of_light(v: torch.Tensor) -> torch.Tensor:
 def bandwidth_probe(kind: str, src: torch.Tensor | None, dst: torch.Tensor) -> None:
     """HBM probe (reference bench/machine.py:41-61): ``read`` streams ``src``
     (``dst`` receives one float per workgroup, see ``probe_grid``), ``write``
-    fills ``dst``, ``copy`` copies ``src`` into ``dst``."""
-    code = {"read": 0, "write": 1, "copy": 2}[kind]
+    fills ``dst``, ``copy`` copies ``src`` into ``dst``, ``mix`` reads ``src``
+    and writes ``dst`` (a ninth of its size) as one linear stream -- the
+    forward's 9:1 read:write ratio without its row stride."""
+    code = {"read": 0, "write": 1, "copy": 2, "mix": 3}[kind]
     nbytes = (src if code != 1 else dst).numel() * (src if code != 1 else dst).element_size()
     with torch.cuda.device(dst.device):
         rc = _lib.lib().sy_bw_probe(code, _ptr(src), _ptr(dst), nbytes, _lib.stream_ptr(dst.device))

@@ -273,11 +273,13 @@ class _Stream:
     def sources(self) -> list[Tensor]:
         return self.blocks if self.running is None else [*self.blocks, self.running]
 
-    def accumulate(self, y: Tensor) -> None:
+    def accumulate(self, y: Tensor, region=contextlib.nullcontext) -> None:
+        """Add a sublayer output to the running sum; in arena mode also copy
+        the new sum into its slot (the staging cost, inside ``region``)."""
         self.running = y if self.running is None else self.running + y
         if self.slots is not None:
             k = len(self.blocks)
-            with torch.no_grad():
+            with region(), torch.no_grad():
                 self.slots[k].copy_(self.running)
             self.holds[k] = self.running
 
@@ -486,7 +488,8 @@ class Transformer(nn.Module):
 
     def _attnres_stream(self, x0: Tensor, collect_alphas: bool) -> Tensor:
         cfg = self.cfg
-        stream = _Stream(x0, cfg.n_blocks, arena=cfg.sources == "arena")
+        with self._region("attnres_stage"):
+            stream = _Stream(x0, cfg.n_blocks, arena=cfg.sources == "arena")
         counts = []
         for i, (norm, fn) in enumerate(self._sublayers()):
             if i > 0 and i % cfg.block_size == 0:
@@ -494,8 +497,7 @@ class Transformer(nn.Module):
             h = self._site(i, stream, collect_alphas)
             counts.append(len(stream.sources()))
             y = fn(norm(h), self.rotary)
-            with self._region("attnres_stage"):
-                stream.accumulate(y)
+            stream.accumulate(y, lambda: self._region("attnres_stage"))
         stream.close_block()
         counts.append(len(stream.sources()))
         self.last_source_counts = counts

@@ -274,8 +274,12 @@ int sy_sol(const void* v, void* out, int64_t n_src, int64_t n_tok, int64_t d,
 /* HBM probes over `bytes` (a multiple of 16): kind 0 = read src (dst receives
  * one float per workgroup, dst must hold sy_probe_grid(bytes) floats, at most
  * 32768),
- * 1 = write dst, 2 = copy src -> dst. Replaces the copy/read/write probes of
- * bench/machine.py:41-61. */
+ * 1 = write dst, 2 = copy src -> dst, 3 = the forward's 9:1 read:write mix as
+ * one linear stream: src holds `bytes` (a multiple of 144), read once in 36 KiB
+ * steps, and dst receives bytes / 9 in 4 KiB steps, each 16-byte chunk the sum
+ * (as 32-bit integers) of the chunks at the same position in the step's nine
+ * 4 KiB source blocks. Replaces the copy/read/write probes of
+ * bench/machine.py:41-61; kind 3 has no reference counterpart. */
 int sy_bw_probe(int kind, const void* src, void* dst, int64_t bytes, void* stream);
 int64_t sy_probe_grid(int64_t bytes);
 

@@ -84,7 +84,8 @@ def test_backward_and_batched_reject_bad_arguments():
     assert lib.sy_sol(_p(FAKE), _p(FAKE), 9, 16, 2048, 16 * 2048, 9, None) == DTYPE
     assert lib.sy_dw_reduce(None, 4, 2048, _p(FAKE), BF16, None) == NULL
     assert lib.sy_dw_reduce(_p(FAKE), 4, 0, _p(FAKE), BF16, None) == SHAPE
-    assert lib.sy_bw_probe(3, _p(FAKE), _p(FAKE), 1024, None) == OP
+    assert lib.sy_bw_probe(4, _p(FAKE), _p(FAKE), 1024, None) == OP
+    assert lib.sy_bw_probe(3, _p(FAKE), _p(FAKE), 1024, None) == SHAPE  # the mix probe reads 144-byte units
     assert lib.sy_bw_probe(0, _p(FAKE), _p(FAKE), 1000, None) == SHAPE
     assert lib.sy_bw_probe(2, None, _p(FAKE), 1024, None) == NULL
     assert lib.sy_bwd_workspace_bytes(0, 16, 2048, BF16, BF16) == SHAPE

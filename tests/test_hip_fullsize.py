@@ -190,3 +190,11 @@ def test_speed_of_light_and_probes():
     out = torch.zeros(probe_grid(src.numel() * 4), device=DEV)
     bandwidth_probe("read", src, out)
     torch.cuda.synchronize()
+    # the 9:1 mix probe: 36 KiB steps in, 4 KiB steps out (one step ragged at the end)
+    steps = 37
+    mix_src = torch.randint(-1000, 1000, (steps * 9 * 1024 - 9 * 4 * 37,), device=DEV, dtype=torch.int32)
+    mix_dst = torch.zeros(mix_src.numel() // 9, device=DEV, dtype=torch.int32)
+    bandwidth_probe("mix", mix_src, mix_dst)
+    full = (steps - 1) * 9 * 1024
+    want = mix_src[:full].view(steps - 1, 9, 256, 4).sum(1).flatten()
+    assert torch.equal(mix_dst[: (steps - 1) * 1024], want)
