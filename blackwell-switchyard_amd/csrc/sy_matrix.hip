@@ -114,7 +114,9 @@ __device__ __forceinline__ void wave_lds_fence() {
 // stands in for rows n >= n_src), then the exchange buffers. KS = D / 128
 // (32-column steps of a wave), NR >= n_src staged rows. Two tokens are in
 // flight per workgroup while a third is computed; the loop is unrolled by two
-// so that both staging sets keep compile-time register indices.
+// so that both staging sets keep compile-time register indices. The loads of a
+// staged token are split around the logits of the current one (half before,
+// half after the exchange barrier), which spreads them over the token.
 //
 // Every global load and store in the loop is issued unconditionally (missing
 // rows load through a zero-size resource, masked lanes store past the end of
@@ -182,17 +184,19 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
 
   // Staging: chunk `lane` of each row of this wave's slice of token t (rows
   // past n_src and tokens past n_tok load zeros through a zero-size resource).
-  auto stage = [&](i32x4_t (&st)[NR], int64_t t) {
+  auto stage_rows = [&](i32x4_t (&st)[NR], int64_t t, int n0, int n1) {
     const bool tok_ok = t < n_tok;
     const int64_t tc = tok_ok ? t : n_tok - 1;
 #pragma unroll
-    for (int n = 0; n < NR; ++n) {
+    for (int n = n0; n < n1; ++n) {
       const bool real = n < n_src && tok_ok;
       const auto r = make_rsrc(row_of<const uint16_t>(v, n < n_src ? n : 0) + tc * d,
                                real ? row_bytes : 0u);
       st[n] = ld16_stream(r, (uint32_t)(cb + 8 * lane) * 2u);
     }
   };
+  auto stage = [&](i32x4_t (&st)[NR], int64_t t) { stage_rows(st, t, 0, NR); };
+  constexpr int kLate = NR / 2;  // rows of the next token loaded after the logits
   auto commit = [&](const i32x4_t (&st)[NR]) {
     wave_lds_fence();
     if (lane < cpr) {
@@ -218,7 +222,7 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
   const uint32_t q_stride = (uint32_t)(n_tok * d * 2);
 
   // One token whose rows are in LDS; k selects the exchange buffer.
-  auto token = [&](int k, int64_t tok) {
+  auto token = [&](int k, int64_t tok, auto&& mid) {
     // Logit and sum-of-squares partials over this wave's columns: row chunks
     // are read kAhead steps ahead of their MFMA, and even and odd steps
     // accumulate in separate chains.
@@ -248,6 +252,7 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
     *(f32x4_t*)&xl[xb][half][w][lane][0] = acc;
     if (lane < kMxRows) xs[xb][half][w][lane] = ss;
     __syncthreads();
+    mid();
     // Lane (g, qi) now holds rows n = 4g + j of query column s = qi.
     f32x4_t pl4[kMxWaves], ps4[kMxWaves];
 #pragma unroll
@@ -382,18 +387,18 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
     __builtin_amdgcn_sched_barrier(0);
     for (int k = 0; k < iters; k += 2) {
       // Token k is in LDS, token k+1 in flight in sb.
-      stage(sa, tok_at(k + 2));
-      token(k, tok_at(k));
+      stage_rows(sa, tok_at(k + 2), 0, NR - kLate);
+      token(k, tok_at(k), [&] { stage_rows(sa, tok_at(k + 2), NR - kLate, NR); });
       if (k + 1 >= iters) break;
       commit(sb);
-      stage(sb, tok_at(k + 3));
-      token(k + 1, tok_at(k + 1));
+      stage_rows(sb, tok_at(k + 3), 0, NR - kLate);
+      token(k + 1, tok_at(k + 1), [&] { stage_rows(sb, tok_at(k + 3), NR - kLate, NR); });
       if (k + 2 < iters) commit(sa);
     }
   } else {
     for (int k = 0; k < iters; ++k) {
       stage(sa, tok_at(k + 1));
-      token(k, tok_at(k));
+      token(k, tok_at(k), [] {});
       if (k + 1 < iters) commit(sa);
     }
   }
