@@ -219,6 +219,43 @@ __device__ __forceinline__ float wave_sum(float x) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
 }
 
+// Sums of 32 per-lane values over the 64 lanes, transposed: lane l ends up
+// with the total of v[tsum32_row(l)], tsum32_row(l) = b0 + 2*b2 + 4*b3 + 8*b4 +
+// 16*b5 of l's bits (lanes l and l ^ 2 hold the same total). Each step halves
+// the values a lane carries: gfx950's permlane32/permlane16 swaps pair the
+// halves across bits 5 and 4, then DPP row rotation by 8, the half-row mirror
+// and two quad permutations pair lanes across bits 3, 2, 0 and 1 -- 70 VALU
+// instructions instead of 32 separate six-step reductions. The order of the
+// adds is fixed, so the result is deterministic.
+__device__ __forceinline__ int tsum32_row(int lane) { return (lane & 1) | ((lane >> 1) & ~1); }
+__device__ __forceinline__ float tsum32(const float (&v)[32], int lane) {
+  float a[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 16]),
+                                                    false, false);
+    a[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);  // n = i + 16*b5
+  }
+  float b[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a[i]), __float_as_uint(a[i + 8]),
+                                                    false, false);
+    b[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);  // n = i + 8*b4 + 16*b5
+  }
+  const bool b3 = (lane & 8) != 0, b2 = (lane & 4) != 0, b0 = (lane & 1) != 0;
+  float c[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)  // row_ror:8 pairs l with l ^ 8
+    c[i] = (b3 ? b[i + 4] : b[i]) + dpp<0x128>(b3 ? b[i] : b[i + 4]);
+  float e[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)  // row_half_mirror pairs l with 7 - l in each 8 lanes
+    e[i] = (b2 ? c[i + 2] : c[i]) + dpp<0x141>(b2 ? c[i] : c[i + 2]);
+  const float f = (b0 ? e[1] : e[0]) + dpp<0xB1>(b0 ? e[0] : e[1]);  // quad_perm [1,0,3,2]
+  return f + dpp<0x4E>(f);                                          // quad_perm [2,3,0,1]
+}
+
 // Max over the 64 lanes, wave-uniform. Rows that a broadcast skips see -inf
 // from the DPP `old` operand, which leaves the max unchanged.
 template <int CTRL, int ROW_MASK = 0xf>

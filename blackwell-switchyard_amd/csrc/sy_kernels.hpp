@@ -973,20 +973,23 @@ k_bwd_tall(const RowTable v, const typename T::storage* __restrict__ w,
       r_next = rinv_of(nxt);
     }
 
-    // G_n = <g, v_n>: this wave's share into lane n, then the W shares of the
-    // token added in segment order through LDS.
+    // G_n = <g, v_n>: this wave's share (transposed sum: row tsum32_row(l) in
+    // lane l), then the W shares of the token added in segment order through
+    // LDS into lane n.
     float gv = 0.0f;
+    {
+      float dts[NR];
 #pragma unroll
-    for (int n = 0; n < NR; ++n) {
-      if (n < opaque(rows)) {
-        float dt = 0.0f;
+      for (int n = 0; n < NR; ++n) {
+        dts[n] = 0.0f;
+        if (n < opaque(rows)) {
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) dt = dot<T>(x[n][j], gq[j], dt);
-        const float s = wave_sum(dt);
-        gv = lane == n ? s : gv;
+          for (int j = 0; j < VPL; ++j) dts[n] = dot<T>(x[n][j], gq[j], dts[n]);
+        }
       }
+      const float s = tsum32(dts, lane);
+      if ((lane & 2) == 0) red[k & 1][slot][seg][tsum32_row(lane)] = s;
     }
-    if (lane < NR) red[k & 1][slot][seg][lane] = gv;
     __syncthreads();
     if (lane < NR) {
       float t = red[k & 1][slot][0][lane];

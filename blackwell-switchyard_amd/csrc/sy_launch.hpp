@@ -23,10 +23,10 @@ namespace sy {
 // which fit only at one wave per SIMD (512 registers, 256-thread workgroups).
 #define SY_BWD_WIDE_TILES(X) X(1, 4, 16) X(2, 4, 16)
 // Backward-only tiles of 32 rows, one or two chunks per lane (128 or 256 tile
-// VGPRs, one wave per SIMD), for 16 < N <= 32 with the forward's stats on stacked rows: the
+// VGPRs; two waves per SIMD, or one), for 16 < N <= 32 with the forward's stats on stacked rows: the
 // operator's gradient as the autograd op calls it. Other callers at that N
 // (no stats, per-row pointers, the (o, m, l) gradient) run the generic kernel.
-#define SY_BWD_TALL_TILES(X) X(2, 1, 32) X(4, 1, 32) X(4, 2, 32)
+#define SY_BWD_TALL_TILES(X) X(2, 1, 32) X(4, 1, 32) X(2, 2, 32) X(4, 2, 32)
 constexpr int kTallRows = 32;
 
 // Largest N the generic kernels accept (their per-token scalars live in LDS).

@@ -159,12 +159,15 @@ int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_
   // would share a SIMD and spill. The 16-row tile holds 256 VGPRs of source
   // rows: its recompute variant (no stats) spills 68 bytes a lane and still
   // beats the thinner tiles (N=16: 119 vs 167 us).
-  // 16 < N <= 32 with the forward's stats: 32 rows resident at one wave per
-  // SIMD, one chunk per lane on two or four waves, or two chunks on four
-  // (v read once; the generic kernel reads it twice with element-wise loads).
+  // 16 < N <= 32 with the forward's stats: 32 rows resident, a token on as
+  // few waves as the registers allow -- two waves with one or two chunks a
+  // lane, four with two from 512 chunks on (v read once; the generic kernel
+  // reads it twice with element-wise loads). At N=32, D=2048 bf16 two waves
+  // of two chunks run the backward in 207 us against 237 us for four waves of
+  // one (fewer waves share each row's loads and each token's barrier).
   // Without stats the per-row scalars would not fit; that case stays generic.
   if (vec && op == SY_OP_BWD && has_stats && n_src > 16 && n_src <= kTallRows && e > 64) {
-    const int ww = e <= 128 ? 2 : 4, vv = e <= 256 ? 1 : 2;
+    const int ww = e <= 256 ? 2 : 4, vv = e <= 128 ? 1 : 2;
     if (e <= 512) {
       set(out, SY_FAMILY_RESIDENT, ww, vv, kTallRows, ce, op, n_src);
       return SY_OK;

@@ -213,9 +213,9 @@ def test_large_n_forward_uses_online_chunks_and_backward_the_32_row_tile():
     assert f["family_name"] == "chunked" and f["n_chunks"] == 3
     assert plan(_lib.OP_FWD, 17, 2048)["family_name"] == "chunked"
     # 16 < N <= 32 (with the forward's stats): 32 rows resident
-    for n, d, dt, tile in ((17, 2048, torch.bfloat16, (4, 1, 32)), (32, 2048, torch.bfloat16, (4, 1, 32)),
+    for n, d, dt, tile in ((17, 2048, torch.bfloat16, (2, 2, 32)), (32, 2048, torch.bfloat16, (2, 2, 32)),
                            (24, 1024, torch.float16, (2, 1, 32)), (32, 4096, torch.bfloat16, (4, 2, 32)),
-                           (32, 2048, torch.float32, (4, 2, 32))):
+                           (32, 2048, torch.float32, (4, 2, 32)), (20, 1024, torch.float32, (2, 2, 32))):
         p = plan(_lib.OP_BWD, n, d, dt)
         assert p["family_name"] == "resident", (n, d)
         assert (p["waves_per_token"], p["chunks_per_lane"], p["rows_per_tile"]) == tile

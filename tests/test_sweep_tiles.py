@@ -71,8 +71,8 @@ SWEEP_CASES = [
     ((9, 4, 256, 1024), ("resident", (1, 2, 9)), (1, 2, 9)),
     ((9, 4, 256, 4096), ("resident", (2, 4, 9)), (2, 4, 9)),
     # 16 < N <= 32: the 32-row backward tile (the reference's n-sweep has N=32)
-    ((32, 1, 4096, 2048), ("chunked", (1, 4, 4)), (4, 1, 32)),
-    ((17, 1, 4 * 256, 2048), ("chunked", (1, 4, 4)), (4, 1, 32)),
+    ((32, 1, 4096, 2048), ("chunked", (1, 4, 4)), (2, 2, 32)),
+    ((17, 1, 4 * 256, 2048), ("chunked", (1, 4, 4)), (2, 2, 32)),
     ((24, 4, 256, 1024), ("chunked", (1, 2, 16)), (2, 1, 32)),
     ((32, 1, 1024, 4096), ("chunked", (2, 4, 4)), (4, 2, 32)),
 ]
@@ -95,9 +95,9 @@ def test_sweep_shape_runs_its_tile_at_the_oracle_floor(shape, fwd, bwd, dtype):
 
 @pytest.mark.parametrize("n,t,d", [(32, 1024, 2048), (19, 600, 1024)])
 def test_32_row_tile_in_fp32(n, t, d):
-    """fp32 rows take the two-chunk 32-row tile at D=2048 (512 chunks) and the
-    one-chunk tile at D=1024; bar: the reference's fp32 tolerance."""
-    tile = (4, 2, 32) if d == 2048 else (4, 1, 32)
+    """fp32 rows take the four-wave 32-row tile at D=2048 (512 chunks) and the
+    two-wave one at D=1024; bar: the reference's fp32 tolerance."""
+    tile = (4, 2, 32) if d == 2048 else (2, 2, 32)
     assert _tile(_lib.OP_BWD, n, d, torch.float32, t) == ("resident", tile)
     gen = torch.Generator().manual_seed(n)
     v = torch.randn(n, 1, t, d, generator=gen)
