@@ -254,21 +254,42 @@ class DecoderLayer(nn.Module):
 # --------------------------------------------------------------------------
 
 
+class _SlotBuffer:
+    """The arena of one forward: ``[n_blocks + 1, B, T, D]`` slots and, per
+    slot, the running-sum value it carries now. Everything the backward keeps
+    (HIP sites hold the buffer, saved-tensor hooks the buffer and a value)
+    lives here, and none of it belongs to the autograd graph: the values are
+    detached aliases and the buffer is written under ``no_grad``. A reference
+    from saved state back into the graph would close a cycle through
+    autograd's C++ nodes, which Python's garbage collector cannot see, and
+    leak every forward's activations."""
+
+    def __init__(self, x0: Tensor, n_blocks: int) -> None:
+        self.slots = x0.new_empty((n_blocks + 1, *x0.shape))
+        self.holds: dict[int, Tensor] = {}
+        self.write(0, x0.detach())
+
+    def write(self, k: int, value: Tensor) -> None:
+        with torch.no_grad():
+            self.slots[k].copy_(value)
+        self.holds[k] = value
+
+    def restore(self, k: int, value: Tensor) -> None:
+        if self.holds.get(k) is not value:
+            self.write(k, value)
+
+
 class _Stream:
     """The residual stream of one AttnRes forward: completed block
-    representations, the running sum, and (arena mode) the slot buffer that
-    mirrors them. ``holds[k]`` is the running-sum tensor whose bytes slot
-    ``k`` currently carries."""
+    representations, the running sum of the current block, and (arena mode)
+    the slot buffer that mirrors them, with ``running_alias`` the detached
+    alias the buffer's running slot was written from."""
 
     def __init__(self, x0: Tensor, n_blocks: int, arena: bool) -> None:
         self.blocks: list[Tensor] = [x0]
         self.running: Tensor | None = None
-        self.slots: Tensor | None = None
-        self.holds: dict[int, Tensor] = {}
-        if arena:
-            self.slots = x0.new_empty((n_blocks + 1, *x0.shape))
-            with torch.no_grad():
-                self.slots[0].copy_(x0)
+        self.running_alias: Tensor | None = None
+        self.buf = _SlotBuffer(x0, n_blocks) if arena else None
 
     def sources(self) -> list[Tensor]:
         return self.blocks if self.running is None else [*self.blocks, self.running]
@@ -277,38 +298,31 @@ class _Stream:
         """Add a sublayer output to the running sum; in arena mode also copy
         the new sum into its slot (the staging cost, inside ``region``)."""
         self.running = y if self.running is None else self.running + y
-        if self.slots is not None:
-            k = len(self.blocks)
-            with region(), torch.no_grad():
-                self.slots[k].copy_(self.running)
-            self.holds[k] = self.running
+        if self.buf is not None:
+            self.running_alias = self.running.detach()
+            with region():
+                self.buf.write(len(self.blocks), self.running_alias)
 
     def close_block(self) -> None:
         self.blocks.append(self.running)
-        self.running = None
+        self.running = self.running_alias = None
 
-    # -- eager sites: saved-tensor hooks over the slot buffer ----------------
-
-    def restore(self, k: int, value: Tensor) -> None:
-        if self.holds.get(k) is not value:
-            with torch.no_grad():
-                self.slots[k].copy_(value)
-            self.holds[k] = value
-
-    def saving(self, running: Tensor | None):
-        """Hooks under which an eager site may save views of the buffer."""
-        storage = self.slots.untyped_storage().data_ptr()
-        slot = len(self.blocks)
+    def saving(self):
+        """Hooks under which an eager site may save views of the buffer: a
+        saved view is kept detached, with the value its running slot held,
+        and the slot is restored before the view is handed back."""
+        buf, slot, value = self.buf, len(self.blocks), self.running_alias
+        storage = buf.slots.untyped_storage().data_ptr()
 
         def pack(t: Tensor):
-            if running is not None and t.untyped_storage().data_ptr() == storage:
-                return (_BufferView, t, slot, running)
+            if value is not None and t.untyped_storage().data_ptr() == storage:
+                return (_BufferView, t.detach(), slot, value)
             return t
 
         def unpack(x):
             if isinstance(x, tuple) and x and x[0] is _BufferView:
-                _, t, k, value = x
-                self.restore(k, value)
+                _, t, k, v = x
+                buf.restore(k, v)
                 return t
             return x
 
@@ -340,7 +354,7 @@ class _SlotSiteHIP(torch.autograd.Function):
         from . import _lib
         from .hip_op import _ptr
 
-        slots = stream.slots
+        slots = stream.buf.slots
         _, b, t, d = slots.shape
         n_tok = b * t
         q = q.contiguous()
@@ -352,7 +366,8 @@ class _SlotSiteHIP(torch.autograd.Function):
                                    _lib.stream_ptr(slots.device))
         _lib.check(rc, "sy_fwd")
         running = stream.running
-        ctx.stream, ctx.n, ctx.eps = stream, n, float(eps)
+        # The buffer, not the stream: the stream holds graph tensors.
+        ctx.buf, ctx.n, ctx.eps = stream.buf, n, float(eps)
         ctx.n_fixed = n - (1 if running is not None else 0)
         ctx.save_for_backward(q, stats, *((running,) if running is not None else ()))
         return out
@@ -363,8 +378,8 @@ class _SlotSiteHIP(torch.autograd.Function):
         from .hip_op import _ptr
 
         q, stats, *running = ctx.saved_tensors
-        stream, n = ctx.stream, ctx.n
-        slots = stream.slots
+        buf, n = ctx.buf, ctx.n
+        slots = buf.slots
         _, b, t, d = slots.shape
         n_tok = b * t
         dev, dt = slots.device, slots.dtype
@@ -387,7 +402,7 @@ class _SlotSiteHIP(torch.autograd.Function):
                 what = "sy_bwd_table"
             else:
                 if running:
-                    stream.restore(n - 1, running[0])
+                    buf.restore(n - 1, running[0].detach())
                 rc = lib.sy_bwd(_ptr(slots), _ptr(q), _ptr(grad_out), _ptr(stats), _ptr(dv), _ptr(dq),
                                 _ptr(ws), ws.numel() * 4, n, n_tok, d, n_tok * d, vt, wt, ctx.eps, st)
                 what = "sy_bwd"
@@ -522,8 +537,8 @@ class Transformer(nn.Module):
         with self._region("attnres_op"):
             if hip:
                 return _SlotSiteHIP.apply(q, stream, n, cfg.norm_eps, *sources)
-            with stream.saving(stream.running):
-                return folded_form(_BufferView.apply(stream.slots, n, *sources), q, cfg.norm_eps)
+            with stream.saving():
+                return folded_form(_BufferView.apply(stream.buf.slots, n, *sources), q, cfg.norm_eps)
 
     def _region(self, name: str):
         return torch.profiler.record_function(name) if self.profile_regions else contextlib.nullcontext()

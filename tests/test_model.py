@@ -133,7 +133,57 @@ def test_framework_modes_overfit_a_fixed_batch(residual):  # :190-208
     assert torch.isfinite(loss) and loss.item() < 0.5 * first
 
 
+def _live(cls):
+    import gc
+
+    gc.collect()
+    return sum(type(o) is cls for o in gc.get_objects())
+
+
+def _steps_leave_no_stream(residual, sources, dev):
+    """A forward keeps its stream (block tensors, running sums, slot buffer)
+    only until its backward has run: anything the backward keeps that points
+    back into the autograd graph would form a cycle through autograd's C++
+    nodes, invisible to Python's collector, and leak one forward's activations
+    per step."""
+    from switchyard.model import _SlotBuffer, _Stream
+
+    m = _build(residual, sources, dev)
+    idx, tgt = _batch(dev)
+    before = (_live(_Stream), _live(_SlotBuffer))
+    for _ in range(3):
+        m.zero_grad(set_to_none=True)
+        m(idx, tgt)[1].backward()  # the logits, kept, would keep the graph
+    assert (_live(_Stream), _live(_SlotBuffer)) == before
+
+
+@pytest.mark.parametrize("sources", ["arena", "stack"])
+def test_framework_steps_free_their_stream(sources):
+    _steps_leave_no_stream("attnres", sources, "cpu")
+
+
 # -- the HIP operator inside the model (GPU) --------------------------------
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not HAS_GPU, reason="needs a HIP device")
+@pytest.mark.parametrize("sources", ["arena", "table", "stack"])
+def test_hip_steps_free_their_stream_and_device_memory(sources):
+    _steps_leave_no_stream("switchyard", sources, "cuda")
+    m = _build("switchyard", sources, "cuda")
+    idx, tgt = _batch("cuda")
+
+    def step():
+        m.zero_grad(set_to_none=True)
+        m(idx, tgt)[1].backward()
+
+    step()
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated()
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    assert torch.cuda.memory_allocated() == base
 
 
 @pytest.mark.gpu
