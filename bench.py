@@ -573,27 +573,33 @@ def sweep_mode(args):
         if args.quick:
             _copy_probe_calibration(torch, dev)
         return
-    n, b, t, d, q = 9, 1, 4096, 2048, 8
+    # Then the reference's query-count sweep around it (docs/batched_queries.md:16-22):
+    # Q = 1, 2, 4 and 16 queries against the same sources.
+    n, b, t, d = 9, 1, 4096, 2048
     nt = b * t
+    ref_us = {1: 121.0, 2: 133.0, 4: 152.0, 8: 198.7, 16: 369.0}
+    qmax = 16
     sets = [dict(v=torch.randn(n, b, t, d, device=dev, generator=gen).to(dt),
-                 out=torch.empty(q, b, t, d, device=dev, dtype=dt)) for _ in range(6)]
+                 out=torch.empty(qmax, b, t, d, device=dev, dtype=dt)) for _ in range(6)]
     gq = torch.Generator().manual_seed(1)
-    queries = (0.5 * torch.randn(q, d, generator=gq)).to(dt).to(dev)
+    all_queries = (0.5 * torch.randn(qmax, d, generator=gq)).to(dt).to(dev)
+    for q in (8, 1, 2, 4, 16):
+        queries = all_queries[:q].contiguous()
 
-    def batched(s):
-        _lib.check(lib.sy_fwd_batched(P(s["v"]), P(queries), P(s["out"]), n, q, nt, d, nt * d, code, 1e-6, st),
-                   "sy_fwd_batched")
+        def batched(s, q=q, queries=queries):
+            _lib.check(lib.sy_fwd_batched(P(s["v"]), P(queries), P(s["out"]), n, q, nt, d, nt * d, code, 1e-6,
+                                          st), "sy_fwd_batched")
 
-    for s in sets:  # warm-up: first launches load code objects and query attributes
-        batched(s)
-    ms = harness.time_loop_median([lambda s=s: batched(s) for s in sets], device=dev, iters=100)
-    nbytes = attn_res_batched_bytes(n, q, b, t, d, item)
-    rec = {"sweep": "batched", "impl": "switchyard_hip", "N": n, "B": b, "T": t, "D": d, "Q": q, "dtype": tag,
-           "fwd_us": round(ms * 1e3, 2), "fwd_gbps": round(nbytes / ms / 1e6, 1),
-           "fwd_frac_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBPS, 4),
-           "reference_rtx_pro_6000_us": 198.7 if tag == "bf16" else None}
-    print(json.dumps(rec), flush=True)
-    results.append(rec)
+        for s in sets:  # warm-up: first launches load code objects and query attributes
+            batched(s)
+        ms = harness.time_loop_median([lambda s=s: batched(s) for s in sets], device=dev, iters=100)
+        nbytes = attn_res_batched_bytes(n, q, b, t, d, item)
+        rec = {"sweep": "batched" if q == 8 else "batched-q", "impl": "switchyard_hip", "N": n, "B": b, "T": t,
+               "D": d, "Q": q, "dtype": tag, "fwd_us": round(ms * 1e3, 2), "fwd_gbps": round(nbytes / ms / 1e6, 1),
+               "fwd_frac_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBPS, 4),
+               "reference_rtx_pro_6000_us": ref_us[q] if tag == "bf16" else None}
+        print(json.dumps(rec), flush=True)
+        results.append(rec)
     if args.json_out:
         args.json_out.parent.mkdir(parents=True, exist_ok=True)
         args.json_out.write_text(json.dumps({"environment": harness.environment(), "dtype": tag,

@@ -42,10 +42,11 @@ constexpr int64_t kBwdBatchedMaxQ = 8;
 // registers). Its stores address four query rows from one buffer resource, so
 // 4 * n_tok * D * 2 bytes must stay below 2^31 (else the per-query path runs).
 // Below kMatrixMinQ queries the register-tiled kernel is faster (config 3
-// shape, MI355X: 2 queries 38.0 vs 67.9 us; 8 queries 82.5 vs 75.5 us).
+// shape, MI355X, register tile vs matrix cores: 2 queries 38.4 vs 50.0 us, 3:
+// 46.4 vs 50.8, 4: 53.5 vs 52.4, 5: 60.4 vs 53.8).
 constexpr int64_t kMatrixMaxRows = 16;
 constexpr int64_t kMatrixMaxQ = 16;
-constexpr int64_t kMatrixMinQ = 6;
+constexpr int64_t kMatrixMinQ = 4;
 inline bool matrix_batched_fits(int64_t n_src, int64_t n_q, int64_t d, int dtype) {
   return (dtype == SY_BF16 || dtype == SY_F16) && n_src >= 1 && n_src <= kMatrixMaxRows &&
          n_q >= kMatrixMinQ && n_q <= kMatrixMaxQ &&

@@ -24,7 +24,7 @@
 //     tile spills and the thinner one is kept.
 //     16 < N <= 32 with stats: the 32-row tile, one chunk per lane on the 2 or
 //     4 waves that cover the row, or two chunks on 4 (D = 4096 in bf16).
-//  5. Batched: 16-bit inputs with N <= 16, 6 <= S <= 16 and D in {512, 1024,
+//  5. Batched: 16-bit inputs with N <= 16, 4 <= S <= 16 and D in {512, 1024,
 //     1536, 2048} run on the matrix cores (config 3: 8 queries x 9 rows is ~7000
 //     VALU instructions a token on the register tile); otherwise resident with
 //     S <= 16, else one forward launch per query.

@@ -245,9 +245,9 @@ def test_batched_matrix_core_plan_bounds():
     fam = lambda n, d, s, dt=torch.bfloat16: plan(_lib.OP_BATCHED, n, d, dt, n_q=s)["family_name"]
     for dt in (torch.bfloat16, torch.float16):
         for d in (512, 1024, 1536, 2048):
-            assert fam(1, d, 6, dt) == "matrix"
+            assert fam(1, d, 4, dt) == "matrix"
             assert fam(16, d, 16, dt) == "matrix"
-    assert fam(9, 2048, 5) == "resident"  # few queries: the register tile is faster
+    assert fam(9, 2048, 3) == "resident"  # few queries: the register tile is faster
     assert fam(17, 2048, 8) != "matrix"
     assert fam(9, 4096, 8) == "resident"
     assert fam(9, 256, 8) == "resident"

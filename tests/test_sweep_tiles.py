@@ -145,3 +145,23 @@ def test_32_row_tile_is_bitwise_deterministic_and_other_callers_fall_back():
     rdv, rdw = c_oracle.backward(v64, w.double().cpu().numpy(), g.double()[0].cpu().numpy())
     for got, ref in ((dv[:, 0], torch.from_numpy(rdv)), (dw, torch.from_numpy(rdw))):
         assert rel_l2(got.cpu(), ref) <= 1.10 * dtype_floor(ref, torch.bfloat16)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("n_q,family", [(1, "resident"), (2, "resident"), (4, "matrix"), (16, "matrix")])
+def test_query_sweep_shapes_at_the_oracle_floor(n_q, family, dtype):
+    """The batched forward at the query-sweep counts (the config-3 sweep's
+    Q = 1, 2, 4, 16 next to Q = 8) on the plan the sweep times, against the
+    float64 C oracle at the 1.10x floor."""
+    from switchyard.triton_op import block_attn_res_batched
+
+    n, t, d = 9, 4 * CUS, 2048
+    assert _lib.plan(_lib.OP_BATCHED, n, d, dtype, n_q=n_q)["family_name"] == family
+    gen = torch.Generator().manual_seed(40 + n_q)
+    v = torch.randn(n, 1, t, d, generator=gen).to(dtype)
+    q = (0.5 * torch.randn(n_q, d, generator=gen)).to(dtype)
+    got = block_attn_res_batched(v.to(DEV), q.to(DEV)).reshape(n_q, t, d).cpu()
+    ref = torch.from_numpy(c_oracle.batched(v.double()[:, 0].numpy(), q.double().numpy()))
+    for i in range(n_q):
+        err, floor = rel_l2(got[i], ref[i]), dtype_floor(ref[i], dtype)
+        assert err <= 1.10 * floor, f"query {i}: rel_l2 {err:.4e} vs floor {floor:.4e}"
