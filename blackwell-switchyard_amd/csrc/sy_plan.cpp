@@ -154,9 +154,11 @@ int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_
     return SY_OK;
   }
   // Four chunks per lane at one wave per SIMD pay off from 5 rows on (N=9:
-  // 62.2 vs 64.9 us); with N <= 4 two chunks on twice the waves are faster
-  // (N=4: 36.4 vs 38.4 us, N=2: 24.6 vs 27.7 us). Eight waves of such a tile
-  // would share a SIMD and spill. The 16-row tile holds 256 VGPRs of source
+  // 62.2 vs 64.9 us), and from 2 rows on for 16-bit sources (T=4096 bf16,
+  // D=2048: N=2 17.4 vs 18.5 us, N=4 28.5 vs 30.2; D=4096: N=4 52.6 vs 56.1;
+  // D=8192: N=4 101.1 vs 109.3). With fp32 sources and N <= 4 two chunks on
+  // twice the waves stay faster (D=2048, N=4: 52.6 vs 58.1 us). Eight waves
+  // of such a tile would share a SIMD and spill. The 16-row tile holds 256 VGPRs of source
   // rows: its recompute variant (no stats) spills 68 bytes a lane and still
   // beats the thinner tiles (N=16: 119 vs 167 us).
   // 16 < N <= 32 with the forward's stats: 32 rows resident, a token on as
@@ -173,11 +175,11 @@ int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_
       return SY_OK;
     }
   }
-  if (vec && op == SY_OP_BWD && n_src > 4 && n_src <= 16) {
+  if (vec && op == SY_OP_BWD && (n_src > 4 || (n_src >= 2 && ce == 8)) && n_src <= 16) {
     for (int ww : {1, 2, 4}) {
       if (n_src > 9 && ww == 4) break;
       if (e > 64 * 2 * ww && e <= 64 * 4 * ww) {
-        set(out, SY_FAMILY_RESIDENT, ww, 4, n_src <= 9 ? 9 : 16, ce, op, n_src);
+        set(out, SY_FAMILY_RESIDENT, ww, 4, n_src <= 4 ? 4 : n_src <= 9 ? 9 : 16, ce, op, n_src);
         return SY_OK;
       }
     }

@@ -269,7 +269,8 @@ def test_backward_takes_four_chunks_only_with_one_wave_per_simd():
                 if p["family_name"] != "resident":
                     continue
                 if p["chunks_per_lane"] == 4:
-                    assert 5 <= n <= 16 and p["rows_per_tile"] == (9 if n <= 9 else 16), (n, d, dt, p)
+                    assert 5 <= n <= 16 or (n >= 2 and dt != torch.float32), (n, d, dt, p)
+                    assert p["rows_per_tile"] == (4 if n <= 4 else 9 if n <= 9 else 16), (n, d, dt, p)
                     assert p["waves_per_token"] <= (4 if n <= 9 else 2), (n, d, dt, p)
                     assert p["block_threads"] == 256, (n, d, dt, p)
                     assert p["tokens_per_block"] * p["waves_per_token"] == 4
@@ -282,7 +283,10 @@ def test_backward_takes_four_chunks_only_with_one_wave_per_simd():
     assert tile(plan(_lib.OP_BWD, 9, 2048, torch.float32)) == (2, 4, 9)
     assert tile(plan(_lib.OP_BWD, 9, 8192)) == (4, 4, 9)
     assert tile(plan(_lib.OP_BWD, 9, 16384))[1] <= 2  # eight such waves would share a SIMD
-    assert tile(plan(_lib.OP_BWD, 4, 2048)) == (2, 2, 4)  # few rows: two waves of two chunks
+    assert tile(plan(_lib.OP_BWD, 4, 2048)) == (1, 4, 4)  # few rows, 16-bit: still four chunks
+    assert tile(plan(_lib.OP_BWD, 2, 8192)) == (4, 4, 4)
+    assert tile(plan(_lib.OP_BWD, 4, 2048, torch.float32)) == (4, 2, 4)  # fp32: two chunks
+    assert tile(plan(_lib.OP_BWD, 1, 2048))[1] <= 2
     assert tile(plan(_lib.OP_BWD, 16, 2048)) == (1, 4, 16)
     assert tile(plan(_lib.OP_BWD, 12, 2048)) == (1, 4, 16)
     assert tile(plan(_lib.OP_BWD, 16, 4096)) == (2, 4, 16)

@@ -61,8 +61,8 @@ def _check(n, b, t, d, dtype, seed):
 # (n, b, t, d): expected (forward family, tile), (backward tile)
 SWEEP_CASES = [
     # N sweep, B=1 T=4096 D=2048 (config 4)
-    ((2, 1, 4096, 2048), ("resident", (1, 4, 4)), (2, 2, 4)),
-    ((4, 1, 4096, 2048), ("resident", (1, 4, 4)), (2, 2, 4)),
+    ((2, 1, 4096, 2048), ("resident", (1, 4, 4)), (1, 4, 4)),
+    ((4, 1, 4096, 2048), ("resident", (1, 4, 4)), (1, 4, 4)),
     ((16, 1, 4096, 2048), ("chunked", (1, 4, 4)), (1, 4, 16)),
     # N between the sweep points: the 16-row backward with a partly filled tile
     ((12, 1, 4 * 256, 2048), ("chunked", (1, 4, 4)), (1, 4, 16)),
