@@ -219,42 +219,93 @@ __device__ __forceinline__ float wave_sum(float x) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
 }
 
-// Sums of 32 per-lane values over the 64 lanes, transposed: lane l ends up
-// with the total of v[tsum32_row(l)], tsum32_row(l) = b0 + 2*b2 + 4*b3 + 8*b4 +
-// 16*b5 of l's bits (lanes l and l ^ 2 hold the same total). Each step halves
-// the values a lane carries: gfx950's permlane32/permlane16 swaps pair the
-// halves across bits 5 and 4, then DPP row rotation by 8, the half-row mirror
-// and two quad permutations pair lanes across bits 3, 2, 0 and 1 -- 70 VALU
-// instructions instead of 32 separate six-step reductions. The order of the
-// adds is fixed, so the result is deterministic.
-__device__ __forceinline__ int tsum32_row(int lane) { return (lane & 1) | ((lane >> 1) & ~1); }
-__device__ __forceinline__ float tsum32(const float (&v)[32], int lane) {
-  float a[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 16]),
-                                                    false, false);
-    a[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);  // n = i + 16*b5
-  }
-  float b[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a[i]), __float_as_uint(a[i + 8]),
-                                                    false, false);
-    b[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);  // n = i + 8*b4 + 16*b5
-  }
-  const bool b3 = (lane & 8) != 0, b2 = (lane & 4) != 0, b0 = (lane & 1) != 0;
-  float c[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)  // row_ror:8 pairs l with l ^ 8
-    c[i] = (b3 ? b[i + 4] : b[i]) + dpp<0x128>(b3 ? b[i] : b[i + 4]);
-  float e[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)  // row_half_mirror pairs l with 7 - l in each 8 lanes
-    e[i] = (b2 ? c[i + 2] : c[i]) + dpp<0x141>(b2 ? c[i] : c[i + 2]);
-  const float f = (b0 ? e[1] : e[0]) + dpp<0xB1>(b0 ? e[0] : e[1]);  // quad_perm [1,0,3,2]
-  return f + dpp<0x4E>(f);                                          // quad_perm [2,3,0,1]
+// Sums of P per-lane values over the 64 lanes, transposed (P = 2, 4, ..., 32):
+// lane l ends up with the total of v[tsum_row<P>(l)]. Each step halves the
+// values a lane carries: gfx950's permlane32/permlane16 swaps pair the halves
+// across lane bits 5 and 4, then DPP row rotation by 8, the half-row mirror and
+// a quad permutation pair lanes across bits 3, 2 and 0, each taking the next
+// lower bit of the value index; the lane bits left over are summed out by the
+// same DPP steps without a split. So v[n] lands in the lanes l with
+// n = b5..b2 of l for P = 16 (l >> 2), l >> 3 for P = 8, and for P = 32 in
+// n = b0 + 2*b2 + 4*b3 + 8*b4 + 16*b5 -- 70 VALU instructions for 32 values
+// where 32 separate six-step reductions take ~380, 36 for 16. tsum_lane<P>(n)
+// is one lane that holds v[n]'s total. The order of the adds is fixed, so the
+// result is deterministic; lanes that hold the same total hold the same bits
+// within a quad, but may differ by rounding between quads for P <= 8.
+template <int P>
+__device__ __forceinline__ constexpr int tsum_lane(int n) {
+  static_assert(P >= 2 && P <= 32 && (P & (P - 1)) == 0, "P is a power of two in [2, 32]");
+  if constexpr (P == 32) return (n & 1) | ((n >> 1) << 2);
+  return n << (P == 16 ? 2 : P == 8 ? 3 : P == 4 ? 4 : 5);
 }
+template <int P>
+__device__ __forceinline__ int tsum_row(int lane) {
+  if constexpr (P == 32) return (lane & 1) | ((lane >> 1) & ~1);
+  return lane >> (P == 16 ? 2 : P == 8 ? 3 : P == 4 ? 4 : 5);
+}
+template <int P>
+__device__ __forceinline__ float tsum(const float (&v)[P], int lane) {
+  static_assert(P >= 2 && P <= 32 && (P & (P - 1)) == 0, "P is a power of two in [2, 32]");
+  const bool b3 = (lane & 8) != 0, b2 = (lane & 4) != 0, b0 = (lane & 1) != 0;
+  float a[P / 2];
+#pragma unroll
+  for (int i = 0; i < P / 2; ++i) {  // value i + (P/2)*b5
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + P / 2]),
+                                                    false, false);
+    a[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  if constexpr (P == 2) {
+    // one value: halve across bit 4 with the swap on itself, then sum bits 3..0
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a[0]), __float_as_uint(a[0]),
+                                                    false, false);
+    float f = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    f += dpp<0x128>(f);  // row_ror:8
+    f += dpp<0x141>(f);  // row_half_mirror
+    f += dpp<0xB1>(f);
+    return f + dpp<0x4E>(f);
+  } else {
+    float b[P / 4];
+#pragma unroll
+    for (int i = 0; i < P / 4; ++i) {  // value i + (P/4)*b4 + (P/2)*b5
+      const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a[i]), __float_as_uint(a[i + P / 4]),
+                                                      false, false);
+      b[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    if constexpr (P == 4) {
+      float f = b[0] + dpp<0x128>(b[0]);
+      f += dpp<0x141>(f);
+      f += dpp<0xB1>(f);
+      return f + dpp<0x4E>(f);
+    } else {
+      float c[P / 8];
+#pragma unroll
+      for (int i = 0; i < P / 8; ++i)  // row_ror:8 pairs l with l ^ 8
+        c[i] = (b3 ? b[i + P / 8] : b[i]) + dpp<0x128>(b3 ? b[i] : b[i + P / 8]);
+      if constexpr (P == 8) {
+        float f = c[0] + dpp<0x141>(c[0]);
+        f += dpp<0xB1>(f);
+        return f + dpp<0x4E>(f);
+      } else {
+        float e[P / 16];
+#pragma unroll
+        for (int i = 0; i < P / 16; ++i)  // row_half_mirror pairs l with 7 - l in each 8 lanes
+          e[i] = (b2 ? c[i + P / 16] : c[i]) + dpp<0x141>(b2 ? c[i] : c[i + P / 16]);
+        if constexpr (P == 16) {
+          const float f = e[0] + dpp<0xB1>(e[0]);
+          return f + dpp<0x4E>(f);
+        } else {
+          const float f = (b0 ? e[1] : e[0]) + dpp<0xB1>(b0 ? e[0] : e[1]);  // quad_perm [1,0,3,2]
+          return f + dpp<0x4E>(f);                                          // quad_perm [2,3,0,1]
+        }
+      }
+    }
+  }
+}
+__device__ __forceinline__ int tsum32_row(int lane) { return tsum_row<32>(lane); }
+__device__ __forceinline__ float tsum32(const float (&v)[32], int lane) { return tsum<32>(v, lane); }
+
+// Smallest power of two >= x (x >= 1), for sizing a tsum.
+__host__ __device__ constexpr int pow2_at_least(int x) { return x <= 1 ? 1 : 2 * pow2_at_least((x + 1) / 2); }
 
 // Max over the 64 lanes, wave-uniform. Rows that a broadcast skips see -inf
 // from the DPP `old` operand, which leaves the max unchanged.

@@ -7,9 +7,11 @@
 // through the buffer descriptor's range check and are never stored.
 //
 // Per token the kernels need only 2-3 wave-uniform scalars per source row
-// (sum of squares, query dot, grad dot). They are summed with DPP inside each
-// wave; when W > 1 the W partial sums meet in LDS and are added in segment
-// order, so every wave of the token computes bit-identical softmax weights.
+// (sum of squares, query dot, grad dot). Tiles of up to 9 rows sum them all
+// at once with one transposed cross-lane sum (tsum), larger tiles one DPP
+// reduction per scalar; when W > 1 the W partial sums meet in LDS and are added
+// in segment order, so every wave of the token computes bit-identical softmax
+// weights.
 //
 // Reference: src/switchyard/triton_op.py:50-78 (_fwd_resident),
 // :81-117 (_fwd_tiled), :153-191 (_speed_of_light), :194-264 (_bwd_resident),
@@ -72,6 +74,41 @@ __device__ __forceinline__ void cross_wave_sum(float (&vals)[G * NR], int groups
 #pragma unroll
       for (int k = 1; k < W; ++k) s += buf[slot][k][i];
       vals[i] = s;
+    }
+  }
+}
+
+// The same totals from per-lane partials tv[i] (i < G*NR, zero past the live
+// rows) by one transposed sum (tsum): with W == 1 each total is read from the
+// lane that holds it; with W > 1 those lanes publish the wave's partials with
+// one LDS store and, after one barrier, every wave adds the W partials in
+// segment order as cross_wave_sum does. Used for tiles of at most 9 rows: at
+// 16 rows the 16 live partials cost the backward tile registers (N=16, D=2048:
+// backward 97.9 vs 97.0 us), while at 9 rows one tsum replaces 9-18 wave_sums
+// (config 2: backward 56.1 vs 57.2 us, forward 29.3 vs 29.6).
+template <int W, int G, int NR, int TPB, int P>
+__device__ __forceinline__ void row_sums_transposed(const float (&tv)[P], float (&part)[G * NR],
+                                                    int groups, int rows,
+                                                    float (&buf)[TPB][W][G * NR], int slot,
+                                                    int seg, int lane) {
+  static_assert(P >= G * NR, "one value per lane slot");
+  const float s = tsum<P>(tv, lane);
+  if constexpr (W == 1) {
+#pragma unroll
+    for (int i = 0; i < G * NR; ++i)
+      part[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), tsum_lane<P>(i)));
+  } else {
+    const int i = tsum_row<P>(lane);
+    if (lane == tsum_lane<P>(i) && i < G * NR) buf[slot][seg][i] = s;
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < G * NR; ++q) {
+      if (q / NR < groups && q % NR < rows) {
+        float t = buf[slot][0][q];
+#pragma unroll
+        for (int k = 1; k < W; ++k) t += buf[slot][k][q];
+        part[q] = t;
+      }
     }
   }
 }
@@ -434,20 +471,41 @@ k_fwd_res(const RowTable v, const typename T::storage* __restrict__ w,
     const int64_t nxt = tok + slots < n_tok ? tok + slots : n_tok - 1;
 
     float part[2 * NR];
+    if constexpr (NR <= 9) {
+      constexpr int P = pow2_at_least(2 * NR);
+      float tv[P];
 #pragma unroll
-    for (int n = 0; n < NR; ++n) {
-      if (n < opaque(rows)) {
-        float ss = 0.0f, dt = 0.0f;
+      for (int i = 0; i < P; ++i) tv[i] = 0.0f;
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) {
-          ss = dot<T>(x[n][j], x[n][j], ss);
-          dt = dot<T>(x[n][j], wq[j], dt);
+      for (int n = 0; n < NR; ++n) {
+        if (n < opaque(rows)) {
+          float ss = 0.0f, dt = 0.0f;
+#pragma unroll
+          for (int j = 0; j < VPL; ++j) {
+            ss = dot<T>(x[n][j], x[n][j], ss);
+            dt = dot<T>(x[n][j], wq[j], dt);
+          }
+          tv[n] = ss;
+          tv[NR + n] = dt;
         }
-        part[n] = wave_sum(ss);
-        part[NR + n] = wave_sum(dt);
       }
+      row_sums_transposed<W, 2, NR, TPB, P>(tv, part, 2, rows, red[k & 1], slot, seg, lane);
+    } else {
+#pragma unroll
+      for (int n = 0; n < NR; ++n) {
+        if (n < opaque(rows)) {
+          float ss = 0.0f, dt = 0.0f;
+#pragma unroll
+          for (int j = 0; j < VPL; ++j) {
+            ss = dot<T>(x[n][j], x[n][j], ss);
+            dt = dot<T>(x[n][j], wq[j], dt);
+          }
+          part[n] = wave_sum(ss);
+          part[NR + n] = wave_sum(dt);
+        }
+      }
+      if constexpr (W > 1) cross_wave_sum<W, 2, NR, TPB>(part, 2, rows, red[k & 1], slot, seg, lane);
     }
-    if constexpr (W > 1) cross_wave_sum<W, 2, NR, TPB>(part, 2, rows, red[k & 1], slot, seg, lane);
 
     float lg[NR];
     float m = -INFINITY;
@@ -717,26 +775,53 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
     // part[n] grad dot; without stats also part[NR + n] query dot and
     // part[2*NR + n] sum of squares.
     float part[G * NR];
+    if constexpr (NR <= 9) {
+      constexpr int P = pow2_at_least(G * NR);
+      float tv[P];
 #pragma unroll
-    for (int n = 0; n < NR; ++n) {
-      if (n < rows) {
-        float gg = 0.0f;
+      for (int i = 0; i < P; ++i) tv[i] = 0.0f;
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) gg = dot<T>(x[n][j], gq[j], gg);
-        part[n] = wave_sum(gg);
-        if constexpr (!STATS) {
-          float dt = 0.0f, ss = 0.0f;
+      for (int n = 0; n < NR; ++n) {
+        if (n < rows) {
+          float gg = 0.0f;
 #pragma unroll
-          for (int j = 0; j < VPL; ++j) {
-            dt = dot<T>(x[n][j], wq[j], dt);
-            ss = dot<T>(x[n][j], x[n][j], ss);
+          for (int j = 0; j < VPL; ++j) gg = dot<T>(x[n][j], gq[j], gg);
+          tv[n] = gg;
+          if constexpr (!STATS) {
+            float dt = 0.0f, ss = 0.0f;
+#pragma unroll
+            for (int j = 0; j < VPL; ++j) {
+              dt = dot<T>(x[n][j], wq[j], dt);
+              ss = dot<T>(x[n][j], x[n][j], ss);
+            }
+            tv[NR + n] = dt;
+            tv[2 * NR + n] = ss;
           }
-          part[NR + n] = wave_sum(dt);
-          part[2 * NR + n] = wave_sum(ss);
         }
       }
+      row_sums_transposed<W, G, NR, TPB, P>(tv, part, G, rows, red[k & 1], slot, seg, lane);
+    } else {
+#pragma unroll
+      for (int n = 0; n < NR; ++n) {
+        if (n < rows) {
+          float gg = 0.0f;
+#pragma unroll
+          for (int j = 0; j < VPL; ++j) gg = dot<T>(x[n][j], gq[j], gg);
+          part[n] = wave_sum(gg);
+          if constexpr (!STATS) {
+            float dt = 0.0f, ss = 0.0f;
+#pragma unroll
+            for (int j = 0; j < VPL; ++j) {
+              dt = dot<T>(x[n][j], wq[j], dt);
+              ss = dot<T>(x[n][j], x[n][j], ss);
+            }
+            part[NR + n] = wave_sum(dt);
+            part[2 * NR + n] = wave_sum(ss);
+          }
+        }
+      }
+      if constexpr (W > 1) cross_wave_sum<W, G, NR, TPB>(part, G, rows, red[k & 1], slot, seg, lane);
     }
-    if constexpr (W > 1) cross_wave_sum<W, G, NR, TPB>(part, G, rows, red[k & 1], slot, seg, lane);
 
     // gref = G of the row with the largest logit. Measuring G from it makes
     // the softmax backward free of cancellation: G_n - S equals
