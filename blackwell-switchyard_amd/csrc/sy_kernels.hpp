@@ -179,20 +179,41 @@ k_fwd(const RowTable v, const typename T::storage* __restrict__ w,
 
     // part[n] = sum of squares, part[NR + n] = query dot of row c0 + n.
     float part[2 * NR];
+    if constexpr (NR <= 9) {
+      constexpr int P = pow2_at_least(2 * NR);
+      float tv[P];
 #pragma unroll
-    for (int n = 0; n < NR; ++n) {
-      if (n < rows) {
-        float ss = 0.0f, dt = 0.0f;
+      for (int i = 0; i < P; ++i) tv[i] = 0.0f;
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) {
-          ss = dot<T>(x[n][j], x[n][j], ss);
-          dt = dot<T>(x[n][j], wq[j], dt);
+      for (int n = 0; n < NR; ++n) {
+        if (n < rows) {
+          float ss = 0.0f, dt = 0.0f;
+#pragma unroll
+          for (int j = 0; j < VPL; ++j) {
+            ss = dot<T>(x[n][j], x[n][j], ss);
+            dt = dot<T>(x[n][j], wq[j], dt);
+          }
+          tv[n] = ss;
+          tv[NR + n] = dt;
         }
-        part[n] = wave_sum(ss);
-        part[NR + n] = wave_sum(dt);
       }
+      row_sums_transposed<W, 2, NR, TPB, P>(tv, part, 2, rows, red[it & 1], slot, seg, lane);
+    } else {
+#pragma unroll
+      for (int n = 0; n < NR; ++n) {
+        if (n < rows) {
+          float ss = 0.0f, dt = 0.0f;
+#pragma unroll
+          for (int j = 0; j < VPL; ++j) {
+            ss = dot<T>(x[n][j], x[n][j], ss);
+            dt = dot<T>(x[n][j], wq[j], dt);
+          }
+          part[n] = wave_sum(ss);
+          part[NR + n] = wave_sum(dt);
+        }
+      }
+      if constexpr (W > 1) cross_wave_sum<W, 2, NR, TPB>(part, 2, rows, red[it & 1], slot, seg, lane);
     }
-    if constexpr (W > 1) cross_wave_sum<W, 2, NR, TPB>(part, 2, rows, red[it & 1], slot, seg, lane);
 
     float lg[NR];
     float cm = m_run;
@@ -333,17 +354,34 @@ k_batched(const RowTable v, const typename T::storage* __restrict__ q,
     }
   }
   float rinv[NR];
-#pragma unroll
-  for (int n = 0; n < NR; ++n) {
-    if (n < rows) {
-      float ss = 0.0f;
-#pragma unroll
-      for (int j = 0; j < VPL; ++j) ss = dot<T>(x[n][j], x[n][j], ss);
-      rinv[n] = wave_sum(ss);
-    }
-  }
   int it = 0;
-  if constexpr (W > 1) cross_wave_sum<W, 1, NR, TPB>(rinv, 1, rows, red[it++ & 1], slot, seg, lane);
+  if constexpr (NR <= 9) {
+    constexpr int P = pow2_at_least(NR);
+    float tv[P];
+#pragma unroll
+    for (int i = 0; i < P; ++i) tv[i] = 0.0f;
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      if (n < rows) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) ss = dot<T>(x[n][j], x[n][j], ss);
+        tv[n] = ss;
+      }
+    }
+    row_sums_transposed<W, 1, NR, TPB, P>(tv, rinv, 1, rows, red[it++ & 1], slot, seg, lane);
+  } else {
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+      if (n < rows) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) ss = dot<T>(x[n][j], x[n][j], ss);
+        rinv[n] = wave_sum(ss);
+      }
+    }
+    if constexpr (W > 1) cross_wave_sum<W, 1, NR, TPB>(rinv, 1, rows, red[it++ & 1], slot, seg, lane);
+  }
 #pragma unroll
   for (int n = 0; n < NR; ++n)
     if (n < rows) rinv[n] = rsqrtf(fmaf(rinv[n], inv_d, eps));
@@ -354,16 +392,33 @@ k_batched(const RowTable v, const typename T::storage* __restrict__ q,
 #pragma unroll
     for (int j = 0; j < VPL; ++j) qq[j] = ld16(qr, lane_off + j * kStep);
     float lg[NR];
+    if constexpr (NR <= 9) {
+      constexpr int P = pow2_at_least(NR);
+      float tv[P];
 #pragma unroll
-    for (int n = 0; n < NR; ++n) {
-      if (n < rows) {
-        float dt = 0.0f;
+      for (int i = 0; i < P; ++i) tv[i] = 0.0f;
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) dt = dot<T>(x[n][j], qq[j], dt);
-        lg[n] = wave_sum(dt);
+      for (int n = 0; n < NR; ++n) {
+        if (n < rows) {
+          float dt = 0.0f;
+#pragma unroll
+          for (int j = 0; j < VPL; ++j) dt = dot<T>(x[n][j], qq[j], dt);
+          tv[n] = dt;
+        }
       }
+      row_sums_transposed<W, 1, NR, TPB, P>(tv, lg, 1, rows, red[it++ & 1], slot, seg, lane);
+    } else {
+#pragma unroll
+      for (int n = 0; n < NR; ++n) {
+        if (n < rows) {
+          float dt = 0.0f;
+#pragma unroll
+          for (int j = 0; j < VPL; ++j) dt = dot<T>(x[n][j], qq[j], dt);
+          lg[n] = wave_sum(dt);
+        }
+      }
+      if constexpr (W > 1) cross_wave_sum<W, 1, NR, TPB>(lg, 1, rows, red[it++ & 1], slot, seg, lane);
     }
-    if constexpr (W > 1) cross_wave_sum<W, 1, NR, TPB>(lg, 1, rows, red[it++ & 1], slot, seg, lane);
     float m = -INFINITY;
 #pragma unroll
     for (int n = 0; n < NR; ++n)
