@@ -362,12 +362,13 @@ k_dw_reduce(const float* __restrict__ partial, int rows, int d, void* __restrict
 // dw[c] = sum over rows of partial[r][c], 16-byte path (D % 4 == 0, rows
 // 16-byte aligned). A workgroup owns 64 columns: lane l of wave w is column
 // group l % 16 (four columns) and row lane rl = 4w + l / 16, which sums rows
-// rl, rl + 64, rl + 128, ... in that order (four loads in flight per step);
-// the 64 row-lane sums are then added pairwise in a fixed tree (row lane i
-// takes i + 32, then i + 16, ...). Same inputs, same bits.
+// rl, rl + 64, rl + 128, ... in that order (four loads in flight per step).
+// Each wave then adds its four row lanes with two lane swaps (row lane q takes
+// q ^ 2, then q ^ 1: permlane32 / permlane16), and after one barrier wave 0
+// adds the 16 wave sums in wave order. Same inputs, same bits.
 __global__ void __launch_bounds__(1024)
 k_dw_reduce4(const float* __restrict__ partial, int rows, int d, void* __restrict__ dw, int wt) {
-  __shared__ float4 sh[64][16];
+  __shared__ float4 sh[16][16];
   const int lane = threadIdx.x & 63;
   const int cl = lane & 15;
   const int rl = (threadIdx.x >> 6) * 4 + (lane >> 4);
@@ -392,21 +393,30 @@ k_dw_reduce4(const float* __restrict__ partial, int rows, int d, void* __restric
       acc.x += a.x; acc.y += a.y; acc.z += a.z; acc.w += a.w;
     }
   }
-  sh[rl][cl] = acc;
+  // Both halves of a swap end up with (low lanes' value) + (high lanes'), in
+  // that order, so the lanes that meet later hold identical bits.
+  auto pair = [](float x, bool across32) {
+    const uint32_t u = __float_as_uint(x);
+    const auto r = across32 ? __builtin_amdgcn_permlane32_swap(u, u, false, false)
+                            : __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  };
+  acc = make_float4(pair(acc.x, true), pair(acc.y, true), pair(acc.z, true), pair(acc.w, true));
+  acc = make_float4(pair(acc.x, false), pair(acc.y, false), pair(acc.z, false), pair(acc.w, false));
+  const int wave = threadIdx.x >> 6;
+  if (lane < 16) sh[wave][cl] = acc;
+  __syncthreads();
+  if (wave == 0 && lane < 16 && c4 < n4) {
+    float4 t = sh[0][cl];
 #pragma unroll
-  for (int h = 32; h >= 1; h /= 2) {
-    __syncthreads();
-    if (rl < h) {
-      const float4 o = sh[rl + h][cl];
-      acc.x += o.x; acc.y += o.y; acc.z += o.z; acc.w += o.w;
-      sh[rl][cl] = acc;
+    for (int q = 1; q < 16; ++q) {
+      const float4 o = sh[q][cl];
+      t.x += o.x; t.y += o.y; t.z += o.z; t.w += o.w;
     }
-  }
-  if (rl == 0 && c4 < n4) {
-    store_elem(dw, 4 * (int64_t)c4, acc.x, wt);
-    store_elem(dw, 4 * (int64_t)c4 + 1, acc.y, wt);
-    store_elem(dw, 4 * (int64_t)c4 + 2, acc.z, wt);
-    store_elem(dw, 4 * (int64_t)c4 + 3, acc.w, wt);
+    store_elem(dw, 4 * (int64_t)c4, t.x, wt);
+    store_elem(dw, 4 * (int64_t)c4 + 1, t.y, wt);
+    store_elem(dw, 4 * (int64_t)c4 + 2, t.z, wt);
+    store_elem(dw, 4 * (int64_t)c4 + 3, t.w, wt);
   }
 }
 
