@@ -64,6 +64,12 @@ SWEEP_CASES = [
     ((2, 1, 4096, 2048), ("resident", (1, 4, 4)), (1, 4, 4)),
     ((4, 1, 4096, 2048), ("resident", (1, 4, 4)), (1, 4, 4)),
     ((16, 1, 4096, 2048), ("chunked", (1, 4, 4)), (1, 4, 16)),
+    # 2 <= N <= 4 in 16 bits: the four-chunk 4-row backward at every width,
+    # with a partly filled tile at N=3; the 9-row four-wave tile at D=8192
+    ((3, 1, 1024, 2048), ("resident", (1, 4, 4)), (1, 4, 4)),
+    ((2, 1, 1024, 4096), ("resident", (2, 4, 4)), (2, 4, 4)),
+    ((4, 1, 768, 8192), ("resident", (4, 4, 4)), (4, 4, 4)),
+    ((9, 1, 768, 8192), ("resident", (4, 4, 9)), (4, 4, 9)),
     # N between the sweep points: the 16-row backward with a partly filled tile
     ((12, 1, 4 * 256, 2048), ("chunked", (1, 4, 4)), (1, 4, 16)),
     # D sweep tiles (config 4 uses B=4 T=4096; the tile depends only on the
