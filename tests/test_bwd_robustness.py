@@ -80,7 +80,7 @@ def _workspace(n, t, d, dtype, fill=None):
 
 @pytest.mark.parametrize("fill", [None, "garbage", "ones"])
 @pytest.mark.parametrize("shape", [(9, 4096, 2048), (9, 1000, 2048), (4, 333, 1024), (9, 37, 2048),
-                                   (2, 5, 512), (9, 1, 2048)])
+                                   (2, 5, 512), (9, 1, 2048), (3, 1000, 2048), (2, 777, 4096)])
 def test_backward_equals_the_staged_path_whatever_the_workspace_holds(shape, fill):
     n, t, d = shape
     print(f"sy_bwd {shape} workspace {fill}", flush=True)
