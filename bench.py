@@ -85,8 +85,9 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--quick", action="store_true",
                     help="--schedule / --sweep: a few launches per row and a copy-probe calibration "
                          "launch at the end (a rocprofv3 --pmc target)")
-    ap.add_argument("--traffic-set", default="config2", choices=["config2", "schedule", "n32"],
-                    help="--traffic: which kernels and workload the counter runs covered")
+    ap.add_argument("--traffic-set", default="config2", choices=["config2", "schedule", "n32", "n4", "n16"],
+                    help="--traffic: which kernels and workload the counter runs covered (nN: "
+                         "bench.py --sweep --sweep-only NN --quick)")
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--sweep-only", default=None,
                     help="comma list of sweep names (n-sweep, t-sweep, d-sweep, batched) or N<n> shapes")
@@ -440,6 +441,12 @@ def _traffic_kernels(args):
                 ("merge_fwd", "k_merge", "k_merge_bwd", 3 * slab + 6 * 4096 * 4, wl),
                 ("merge_bwd", "k_merge_bwd", None, 5 * slab + 10 * 4096 * 4, wl),
                 ("table_bwd", "true, 1>", None, (2 * n + 1) * slab, wl)]
+    if args.traffic_set in ("n4", "n16"):  # bench.py --sweep --sweep-only N4 (N16) --quick
+        n, d = int(args.traffic_set[1:]), 2048
+        slab = 4096 * d * 2
+        wl = f"N={n} B=1 T=4096 D={d} bf16"
+        fwd = ("fwd", "k_fwd_res", None) if n <= 9 else ("fwd_chunked", "k_fwd<", None)
+        return [(*fwd, (n + 1) * slab, wl), ("bwd_main", "k_bwd<", None, (2 * n + 1) * slab, wl)]
     n, d = 32, 2048  # bench.py --sweep --sweep-only N32 --quick
     slab = 4096 * d * 2
     wl = f"N={n} B=1 T=4096 D={d} bf16"
