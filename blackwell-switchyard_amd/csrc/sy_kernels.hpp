@@ -27,8 +27,7 @@ namespace sy {
 // kept live. The row guards `n < rows` of the resident kernels otherwise
 // become 64-bit predicates held for the whole kernel and spilled into VGPR
 // lanes (the 32-row backward: ~140 SGPR spills; the forward: 46 -> 16 and
-// 30.2 -> 29.8 us at config 2). k_bwd keeps plain guards: there they measured
-// 0.15 us slower.
+// 30.2 -> 29.8 us at config 2; k_bwd up to 9 rows: 55.9 -> 55.6 us).
 __device__ __forceinline__ int opaque(int x) {
   asm volatile("" : "+s"(x));
   return x;
@@ -752,6 +751,12 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
   const int64_t slots = (int64_t)gridDim.x * TPB;
   const int64_t first = (int64_t)blockIdx.x * TPB + slot;
   const int rows = n_src;  // host guarantees n_src <= NR
+  // Row guards: opaque up to 9 rows (backward 55.6 vs 55.9 us at config 2), plain at 16
+  // rows, where the opaque form measured 0.2 us slower.
+  auto live_row = [&](int n) {
+    if constexpr (NR <= 9) return n < opaque(rows);
+    else return n < rows;
+  };
   int iters = n_iter;
   if constexpr (W == 1) {
     // No barrier inside the loop: each wave runs only its own tokens.
@@ -781,7 +786,7 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
     const int64_t t0 = first < n_tok ? first : n_tok - 1;
 #pragma unroll
     for (int n = 0; n < NR; ++n) {
-      if (n < rows) {
+      if (live_row(n)) {
         const auto r = make_rsrc(row_at<LISTED, const S>(v, n) + t0 * d, row_bytes);
 #pragma unroll
         for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
@@ -837,7 +842,7 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
       for (int i = 0; i < P; ++i) tv[i] = 0.0f;
 #pragma unroll
       for (int n = 0; n < NR; ++n) {
-        if (n < rows) {
+        if (live_row(n)) {
           float gg = 0.0f;
 #pragma unroll
           for (int j = 0; j < VPL; ++j) gg = dot<T>(x[n][j], gq[j], gg);
@@ -858,7 +863,7 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
     } else {
 #pragma unroll
       for (int n = 0; n < NR; ++n) {
-        if (n < rows) {
+        if (live_row(n)) {
           float gg = 0.0f;
 #pragma unroll
           for (int j = 0; j < VPL; ++j) gg = dot<T>(x[n][j], gq[j], gg);
@@ -888,7 +893,7 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
     [[maybe_unused]] int top = 0;
 #pragma unroll
     for (int n = 0; n < NR; ++n) {
-      if (n < rows) {
+      if (live_row(n)) {
         if constexpr (STATS) {
           lg[n] = scalar(n);
           rr[n] = scalar(kSL + n);
@@ -907,7 +912,7 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
     float l = 0.0f;
 #pragma unroll
     for (int n = 0; n < NR; ++n)
-      if (n < rows) {
+      if (live_row(n)) {
         al[n] = expf(lg[n] - m);
         l += al[n];
       }
@@ -917,7 +922,7 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
       const float inv_l = 1.0f / l;
 #pragma unroll
       for (int n = 0; n < NR; ++n)
-        if (n < rows) {
+        if (live_row(n)) {
           al[n] *= inv_l;
           part[n] -= gref;
           sdev = fmaf(al[n], part[n], sdev);
@@ -927,7 +932,7 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
       float other = 0.0f;
 #pragma unroll
       for (int n = 0; n < NR; ++n)
-        if (n < rows) {
+        if (live_row(n)) {
           part[n] += glv;
           if (n != top) other = fmaf(al[n], part[n], other);
         }
@@ -949,7 +954,7 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
     const float dw_on = live ? 1.0f : 0.0f;
 #pragma unroll
     for (int n = 0; n < NR; ++n) {
-      if (n < rows) {
+      if (live_row(n)) {
         const float dlogit = al[n] * (part[n] - sdev);
         const float da = dlogit * rr[n];
         const float c = -dlogit * lg[n] * rr[n] * rr[n] * inv_d;
