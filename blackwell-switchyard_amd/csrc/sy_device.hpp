@@ -7,6 +7,12 @@
 // All arithmetic is fp32. Sums of squares and query dot products of 16-bit
 // data use v_dot2_f32_{bf16,f16} (two exact products, fp32 accumulate), which
 // halves the VALU count of the reductions; fp32 data uses plain FMAs.
+//
+// Timings in the comments of these sources are MI355X measurements, bf16
+// unless stated. Named shapes: "config 2" is N=9 sources, B=1, T=4096,
+// D=2048 (the operator's forward and backward); "config 3" the same sources
+// with 8 queries (the batched forward); "config 4" the N / T / D sweeps around
+// config 2; "config 5" the 1.3B decoder training step.
 #pragma once
 
 #include <hip/hip_runtime.h>
