@@ -94,3 +94,17 @@ def test_a_missing_kernel_is_an_error(tmp_path):
                        capture_output=True, text=True, cwd=ROOT, timeout=120)
     assert r.returncode != 0
     assert "no dispatch of" in (r.stdout + r.stderr)
+
+
+def test_summarize_turns_kernel_stats_into_microseconds(tmp_path):
+    d = tmp_path / "trace" / "host"
+    d.mkdir(parents=True)
+    with open(d / "7_kernel_stats.csv", "w", newline="") as fh:
+        w = csv.writer(fh, quoting=csv.QUOTE_ALL)
+        w.writerow(["Name", "Calls", "TotalDurationNs", "AverageNs", "Percentage", "MinNs", "MaxNs", "StdDev"])
+        w.writerow(["void sy::k_bwd<sy::BF16, 1, 4, 9, true, 0>(x)", 490, 27781000, 56696.0, 60.0, 53350.0,
+                    65870.0, 1.0])
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--summarize", str(tmp_path / "trace"),
+                        "--title", "t"], capture_output=True, text=True, cwd=ROOT, timeout=120)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert "| `void sy::k_bwd<sy::BF16, 1, 4, 9, true, 0>(x)` | 490 | 56.70 | 53.35 | 65.87 |" in r.stdout
