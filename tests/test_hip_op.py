@@ -62,6 +62,7 @@ SHAPES = [
     (16, 1, 128, 1024), (17, 1, 64, 2048), (32, 1, 64, 1024), (33, 1, 64, 512),
     (3, 1, 64, 777), (5, 1, 17, 63), (8, 3, 101, 1536), (7, 2, 1, 320),
     (12, 1, 64, 2048), (16, 1, 64, 2048), (16, 1, 32, 4096),
+    (4, 1, 256, 512),  # BASELINE.json configs[0]'s shape on the HIP path
 ]
 
 
