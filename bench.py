@@ -90,7 +90,8 @@ def parse_args() -> argparse.Namespace:
                          "bench.py --sweep --sweep-only NN --quick)")
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--sweep-only", default=None,
-                    help="comma list of sweep names (n-sweep, t-sweep, d-sweep, batched) or N<n> shapes")
+                    help="comma list of sweep names (n-sweep, t-sweep, d-sweep, d-sweep-b1, batch, small, "
+                         "batched) or N<n> for that n-sweep shape")
     ap.add_argument("--schedule", action="store_true")
     ap.add_argument("--model", action="store_true")
     ap.add_argument("--model-scale", default="1.3B", choices=["1.3B", "small"])
@@ -496,8 +497,61 @@ def traffic_mode(args):
 SWEEP_SHAPES = (
     [("n-sweep", n, 1, 4096, 2048) for n in (2, 4, 8, 9, 16, 32)]
     + [("t-sweep", 9, 1, t, 2048) for t in (512, 1024, 2048, 4096, 8192, 16384)]
+    # BASELINE.json configs[3] puts the D sweep at B=4 ...
     + [("d-sweep", 9, 4, 4096, d) for d in (1024, 2048, 4096)]
+    # ... the reference's own shape sets (bench/bench_operator.py:65-79) at B=1,
+    # with its batch and small sets
+    + [("d-sweep-b1", 9, 1, 4096, d) for d in (1024, 2048, 4096, 8192)]
+    + [("batch", 9, b, 2048, 2048) for b in (1, 2, 4, 8)]
+    + [("small", 9, 1, 128, 1024), ("small", 9, 1, 512, 1024), ("small", 4, 1, 256, 512)]
 )
+
+#: The reference's published numbers on its RTX PRO 6000 (docs/results.md:20-60):
+#: (N, B, T, D) -> (forward ms, fwd+bwd ms, forward % of its speed-of-light kernel).
+REFERENCE_RESULTS = {
+    (9, 1, 2048, 2048): (0.070, 0.181, 91), (9, 2, 2048, 2048): (0.125, 0.365, 97),
+    (9, 4, 2048, 2048): (0.229, 0.688, 98), (9, 8, 2048, 2048): (0.440, 1.337, 100),
+    (9, 1, 4096, 1024): (0.068, 0.191, 100), (9, 1, 4096, 2048): (0.123, 0.365, 97),
+    (9, 1, 4096, 4096): (0.242, 0.924, 93), (9, 1, 4096, 8192): (0.522, 1.997, 85),
+    (2, 1, 4096, 2048): (0.037, 0.177, 106), (4, 1, 4096, 2048): (0.066, 0.170, 97),
+    (8, 1, 4096, 2048): (0.106, 0.309, 102), (16, 1, 4096, 2048): (0.197, 0.608, 101),
+    (32, 1, 4096, 2048): (0.379, 1.552, 98), (9, 1, 128, 1024): (0.010, 0.169, 80),
+    (9, 1, 512, 1024): (0.014, 0.112, 86), (4, 1, 256, 512): (0.008, 0.163, 100),
+    (9, 1, 512, 2048): (0.025, 0.175, 75), (9, 1, 8192, 2048): (0.227, 0.686, 98),
+    (9, 1, 16384, 2048): (0.442, 1.335, 99),
+}
+
+#: The reference's eight-query shape checks of the batched forward
+#: (docs/batched_queries.md:27-34): (N, B, T, D) -> its ms on the RTX PRO 6000.
+BATCHED_SHAPE_CHECKS = {
+    (2, 1, 4096, 2048): 0.117, (16, 1, 4096, 2048): 0.344, (9, 1, 4096, 1024): 0.109,
+    (9, 1, 128, 1024): 0.016, (9, 4, 2048, 2048): 0.393, (9, 1, 4096, 4096): 2.241,
+}
+
+
+def _sweep_shapes(only):
+    """Distinct (N, B, T, D) of SWEEP_SHAPES in order, each with the sets that
+    list it. ``only`` keeps a shape when one of its sets is named, or, for
+    n-sweep shapes, when ``N<n>`` is."""
+    shapes: dict[tuple, list[str]] = {}
+    for name, n, b, t, d in SWEEP_SHAPES:
+        shapes.setdefault((n, b, t, d), []).append(name)
+    for shape, names in shapes.items():
+        if only is None or any(x in only for x in names) or ("n-sweep" in names and f"N{shape[0]}" in only):
+            yield shape, names
+
+
+def _gate(tag, got, ref):
+    """Per-tensor float64 check: 16-bit results within 1.10x the dtype floor,
+    fp32 within 1e-5 relative L2 (the north star's bars)."""
+    from switchyard import harness
+
+    rep = harness.check_against(got, ref, rel_l2_tol=1e-5 if tag == "fp32" else float("inf"))
+    if tag != "fp32":
+        ratio = rep["err_vs_dtype_floor"]
+        rep["ok"] = bool(ratio is not None and ratio <= 1.10 and not rep["nan_or_inf"])
+        rep["rel_l2_tol"] = "1.10 x dtype floor"
+    return {k: (round(v, 7) if isinstance(v, float) else v) for k, v in rep.items()}
 
 
 DTYPE_TAG = {"bfloat16": "bf16", "float16": "fp16", "float32": "fp32"}
@@ -521,10 +575,10 @@ def sweep_mode(args):
     item = torch.finfo(dt).bits // 8
     gen = torch.Generator(device=dev).manual_seed(0)
     results = []
+    failed = []
     only = set(args.sweep_only.split(",")) if args.sweep_only else None
-    for name, n, b, t, d in SWEEP_SHAPES:
-        if only is not None and name not in only and f"N{n}" not in only:
-            continue
+    for (n, b, t, d), names in _sweep_shapes(only):
+        name = names[0]
         nt = b * t
         slab = nt * d * item
         rot = max(2, min(6, int((3 << 30) // ((2 * n + 3) * slab))))
@@ -547,6 +601,9 @@ def sweep_mode(args):
             _lib.check(lib.sy_bwd(P(s["v"]), P(w), P(s["g"]), P(s["stats"]), P(s["dv"]), P(s["dw"]), P(ws),
                                   ws_bytes, n, nt, d, nt * d, code, code, 1e-6, st), "sy_bwd")
 
+        def sol(s):  # the ceiling: same bytes and launch shape, out = sum_n v_n
+            _lib.check(lib.sy_sol(P(s["v"]), P(s["out"]), n, nt, d, nt * d, code, st), "sy_sol")
+
         iters = max(20, min(200, int(2e5 / (n * t * b * d / 1e4))))
         for s in sets:  # warm-up: a shape's first launches query kernel attributes
             fwd(s)
@@ -556,61 +613,130 @@ def sweep_mode(args):
             iters = 3
         f_ms = loop([lambda s=s: fwd(s) for s in sets], device=dev, iters=iters)
         fb_ms = loop([lambda s=s: (fwd(s), bwd(s)) for s in sets], device=dev, iters=iters)
+        for s in sets:
+            sol(s)
+        sol_ms = loop([lambda s=s: sol(s) for s in sets], device=dev, iters=iters)
         fb = attn_res_train_bytes(n, b, t, d, item)
         fw = attn_res_min_bytes(n, b, t, d, item)
         fplan = _lib.plan(_lib.OP_FWD, n, d, dt, n_tok=nt)
         bplan = _lib.plan(_lib.OP_BWD, n, d, dt, n_tok=nt)
-        rec = {"sweep": name, "impl": "switchyard_hip", "N": n, "B": b, "T": t, "D": d, "dtype": tag,
-               "rotating_sets": rot,
+        # Float64 gate of the timed launches' own outputs (set 0; same inputs,
+        # same bits as every timed call on it), as the reference's harness
+        # checks every shape before timing it (bench/harness.py:295-358).
+        s0 = sets[0]
+        fwd(s0)
+        bwd(s0)
+        ref_out, ref_dv, ref_dw = harness.float64_operator(s0["v"], w, s0["g"])
+        check = {"out": _gate(tag, s0["out"], ref_out), "dv": _gate(tag, s0["dv"], ref_dv),
+                 "dw": _gate(tag, s0["dw"], ref_dw)}
+        check["ok"] = all(c["ok"] for c in check.values())
+        del ref_out, ref_dv, ref_dw
+        rec = {"sweep": name, "sweeps": names, "impl": "switchyard_hip", "N": n, "B": b, "T": t, "D": d,
+               "dtype": tag, "rotating_sets": rot,
                "fwd_us": round(f_ms * 1e3, 2), "fwd_gbps": round(fw / f_ms / 1e6, 1),
                "fwd_frac_hbm_peak": round(fw / f_ms / 1e6 / HBM_PEAK_GBPS, 4),
+               "sol_us": round(sol_ms * 1e3, 2),
+               "fwd_pct_of_ceiling": round(100 * sol_ms / f_ms, 1),
                "fwd_bwd_us": round(fb_ms * 1e3, 2), "fwd_bwd_gbps": round(fb / fb_ms / 1e6, 1),
                "fwd_bwd_frac_hbm_peak": round(fb / fb_ms / 1e6 / HBM_PEAK_GBPS, 4),
                "workspace_bytes": ws_bytes + 2 * n * nt * 4,
                "fwd_tile": [fplan["family_name"], fplan["waves_per_token"], fplan["chunks_per_lane"],
                             fplan["rows_per_tile"]],
                "bwd_tile": [bplan["family_name"], bplan["waves_per_token"], bplan["chunks_per_lane"],
-                            bplan["rows_per_tile"]]}
+                            bplan["rows_per_tile"]],
+               "check": check}
+        ref = REFERENCE_RESULTS.get((n, b, t, d))
+        if ref is not None and tag == "bf16":
+            rec["reference_rtx_pro_6000"] = {"fwd_us": 1e3 * ref[0], "fwd_bwd_us": 1e3 * ref[1],
+                                             "fwd_pct_of_ceiling": ref[2]}
         print(json.dumps(rec), flush=True)
         results.append(rec)
+        if not check["ok"]:
+            failed.append(f"N{n} B{b} T{t} D{d}")
         del sets, ws
         torch.cuda.empty_cache()
     # Config 3: batched, Q=8 queries sharing one read of v.
-    if only is not None and "batched" not in only:
-        if args.quick:
-            _copy_probe_calibration(torch, dev)
-        return
-    # Then the reference's query-count sweep around it (docs/batched_queries.md:16-22):
-    # Q = 1, 2, 4 and 16 queries against the same sources.
-    n, b, t, d = 9, 1, 4096, 2048
-    nt = b * t
-    ref_us = {1: 121.0, 2: 133.0, 4: 152.0, 8: 198.7, 16: 369.0}
-    qmax = 16
-    sets = [dict(v=torch.randn(n, b, t, d, device=dev, generator=gen).to(dt),
-                 out=torch.empty(qmax, b, t, d, device=dev, dtype=dt)) for _ in range(6)]
-    gq = torch.Generator().manual_seed(1)
-    all_queries = (0.5 * torch.randn(qmax, d, generator=gq)).to(dt).to(dev)
-    for q in (8, 1, 2, 4, 16):
-        queries = all_queries[:q].contiguous()
+    if only is None or "batched" in only:
+        batched_sweep(args, results, failed)
+    elif args.quick:
+        _copy_probe_calibration(torch, dev)
+    if args.json_out:
+        args.json_out.parent.mkdir(parents=True, exist_ok=True)
+        args.json_out.write_text(json.dumps({"environment": harness.environment(), "dtype": tag,
+                                             "results": results}, indent=1))
+    if failed:
+        log(f"bench.py --sweep: float64 gate failed at {', '.join(failed)}")
+        sys.exit(1)
 
-        def batched(s, q=q, queries=queries):
+
+def batched_sweep(args, results, failed):
+    """Config 3 (Q=8 at N=9 B=1 T=4096 D=2048), the reference's query-count
+    sweep around it (Q = 1, 2, 4, 16; docs/batched_queries.md:16-22) and its
+    eight-query shape checks (:27-34), each gated against float64."""
+    import torch
+
+    from switchyard import _lib, harness
+    from switchyard.reference import attn_res_batched_bytes
+
+    dev = torch.device("cuda:0")
+    lib, st = _lib.lib(), _lib.stream_ptr(dev)
+    P = Workload._p
+    dt = getattr(torch, args.dtype)
+    code, tag = _lib.dtype_code(dt), DTYPE_TAG[args.dtype]
+    item = torch.finfo(dt).bits // 8
+    gen = torch.Generator(device=dev).manual_seed(0)
+    gq = torch.Generator().manual_seed(1)  # the reference's query seed (bench/harness.py:68-69)
+    qmax = 16
+    all_queries = (0.5 * torch.randn(qmax, 8192, generator=gq)).to(dt).to(dev)
+    ref_q_us = {1: 121.0, 2: 133.0, 4: 152.0, 8: 198.7, 16: 369.0}
+    cases = [((9, 1, 4096, 2048), q) for q in (8, 1, 2, 4, 16)]
+    cases += [(shape, 8) for shape in BATCHED_SHAPE_CHECKS if shape != (9, 1, 4096, 2048)]
+    prev = None
+    for (n, b, t, d), q in cases:
+        nt = b * t
+        if prev != (n, b, t, d):
+            sets = None
+            torch.cuda.empty_cache()
+            slab = nt * d * item
+            rot = max(2, min(6, int((3 << 30) // ((n + qmax) * slab))))
+            sets = [dict(v=torch.randn(n, b, t, d, device=dev, generator=gen).to(dt),
+                         out=torch.empty(qmax, b, t, d, device=dev, dtype=dt)) for _ in range(rot)]
+            prev = (n, b, t, d)
+        queries = all_queries[:q, :d].contiguous()
+
+        def batched(s, q=q, queries=queries, n=n, nt=nt, d=d):
             _lib.check(lib.sy_fwd_batched(P(s["v"]), P(queries), P(s["out"]), n, q, nt, d, nt * d, code, 1e-6,
                                           st), "sy_fwd_batched")
 
         for s in sets:  # warm-up: first launches load code objects and query attributes
             batched(s)
-        ms = harness.time_loop_median([lambda s=s: batched(s) for s in sets], device=dev, iters=100)
+        iters = 3 if args.quick else max(20, min(100, int(2e5 / ((n + q) * nt * d / 1e4))))
+        loop = harness.time_loop if args.quick else harness.time_loop_median
+        ms = loop([lambda s=s: batched(s) for s in sets], device=dev, iters=iters)
         nbytes = attn_res_batched_bytes(n, q, b, t, d, item)
-        rec = {"sweep": "batched" if q == 8 else "batched-q", "impl": "switchyard_hip", "N": n, "B": b, "T": t,
-               "D": d, "Q": q, "dtype": tag, "fwd_us": round(ms * 1e3, 2), "fwd_gbps": round(nbytes / ms / 1e6, 1),
+        s0 = sets[0]
+        batched(s0)
+        check = {}
+        for k in range(q):
+            ref, _, _ = harness.float64_operator(s0["v"], queries[k])
+            check[f"out[{k}]"] = _gate(tag, s0["out"][k], ref)
+        worst = max(check.values(), key=lambda c: c["rel_l2"])
+        check = {"queries": q, "ok": all(c["ok"] for c in check.values()), "worst": worst}
+        plan = _lib.plan(_lib.OP_BATCHED, n, d, dt, n_q=q)
+        config3 = (n, b, t, d) == (9, 1, 4096, 2048)
+        rec = {"sweep": ("batched" if q == 8 else "batched-q") if config3 else "batched-shape",
+               "impl": "switchyard_hip", "N": n, "B": b, "T": t, "D": d, "Q": q, "dtype": tag,
+               "fwd_us": round(ms * 1e3, 2), "fwd_gbps": round(nbytes / ms / 1e6, 1),
                "fwd_frac_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBPS, 4),
-               "reference_rtx_pro_6000_us": ref_us[q] if tag == "bf16" else None}
+               "family": plan["family_name"], "check": check}
+        if tag == "bf16":
+            rec["reference_rtx_pro_6000_us"] = ref_q_us[q] if config3 else 1e3 * BATCHED_SHAPE_CHECKS[(n, b, t, d)]
         print(json.dumps(rec), flush=True)
         results.append(rec)
-    if args.json_out:
-        args.json_out.parent.mkdir(parents=True, exist_ok=True)
-        args.json_out.write_text(json.dumps({"environment": harness.environment(), "dtype": tag,
-                                             "results": results}, indent=1))
+        if not check["ok"]:
+            failed.append(f"batched N{n} B{b} T{t} D{d} Q{q}")
+    del sets
+    torch.cuda.empty_cache()
 
 
 def schedule_mode(args):

@@ -211,6 +211,48 @@ def achieved_bandwidth_gbps(nbytes: int, ms: float) -> float:
     return nbytes / (ms * 1e-3) / 1e9
 
 
+# ---------------------------------------------------------------------------
+# Per-shape correctness gate of the sweeps
+# ---------------------------------------------------------------------------
+
+
+def float64_operator(v: torch.Tensor, w: torch.Tensor, grad_out: torch.Tensor | None = None,
+                     eps: float = 1e-6):
+    """out (and dv, dw for ``grad_out``) of the operator in float64 on v's
+    device: ``r_n = rsqrt(mean_d v_n^2 + eps)``, ``alpha = softmax_n(r_n <w, v_n>)``,
+    ``out = sum_n alpha_n v_n`` (reference src/switchyard/reference.py:130-133),
+    gradients by autograd. Written with elementwise products and sums only (no
+    batched matrix products), so that it runs on the GPU in float64 at full
+    sweep sizes within seconds. The benchmark's comparator, as the reference's
+    harness compares every shape with its float64 oracle; the test suite's
+    oracle is separate."""
+    v64 = v.detach().to(torch.float64).requires_grad_(grad_out is not None)
+    w64 = w.detach().to(torch.float64).requires_grad_(grad_out is not None)
+    with torch.enable_grad():
+        logit = (v64 * w64).sum(-1) * torch.rsqrt(v64.pow(2).mean(-1) + eps)
+        alpha = torch.softmax(logit, dim=0)
+        out = (alpha.unsqueeze(-1) * v64).sum(0)
+        if grad_out is None:
+            return out.detach(), None, None
+        dv, dw = torch.autograd.grad(out, (v64, w64), grad_out.detach().to(torch.float64))
+    return out.detach(), dv, dw
+
+
+def check_against(got: torch.Tensor, ref: torch.Tensor, *, rel_l2_tol: float) -> dict:
+    """Relative L2 error of ``got`` against a float64 ``ref`` and the error the
+    float64 values themselves take on when rounded to ``got``'s dtype (the
+    dtype floor); the reference's metric (bench/harness.py:295-358)."""
+    o = ref.to(torch.float64)
+    g = got.to(torch.float64)
+    o_norm = o.norm().item()
+    rel = (g - o).norm().item() / o_norm if o_norm > 0 else float("inf")
+    floor = (o.to(got.dtype).to(torch.float64) - o).norm().item() / o_norm if o_norm > 0 else 0.0
+    bad = bool(torch.isnan(got).any().item() or torch.isinf(got).any().item())
+    return {"ok": rel <= rel_l2_tol and not bad, "rel_l2": rel, "rel_l2_tol": rel_l2_tol,
+            "dtype_floor_rel_l2": floor, "err_vs_dtype_floor": rel / floor if floor > 0 else None,
+            "nan_or_inf": bad}
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
