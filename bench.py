@@ -441,6 +441,8 @@ def _traffic_kernels(args):
                 ("batched_bwd", "k_bwd_batched_mx", None, (2 * n + s) * slab + s * d * 2, wl),
                 ("merge_fwd", "k_merge", "k_merge_bwd", 3 * slab + 6 * 4096 * 4, wl),
                 ("merge_bwd", "k_merge_bwd", None, 5 * slab + 10 * 4096 * 4, wl),
+                # the fused phase 2 (5 sources + the prior's o1 in, out written)
+                ("phase2_fused", "4, 9, true>", None, 7 * slab + 4 * 4096 * 4, wl),
                 ("table_bwd", "true, 1>", None, (2 * n + 1) * slab, wl)]
     if args.traffic_set in ("n4", "n16"):  # bench.py --sweep --sweep-only N4 (N16) --quick
         n, d = int(args.traffic_set[1:]), 2048
@@ -848,10 +850,22 @@ def schedule_mode(args):
         stats_fwd(s, split, n, s["o2"], s["m2"], s["l2"])
     emit("merge_fwd", timed([lambda s=s: merge(s) for s in sets]), 3 * slab + 6 * nt * 4)
     emit("merge_bwd", timed([lambda s=s: merge_bwd(s) for s in sets]), 5 * slab + 10 * nt * 4)
-    emit("two_phase_fwd", timed([lambda s=s: (stats_fwd(s, 0, split, s["o1"], s["m1"], s["l1"]),
-                                              stats_fwd(s, split, n, s["o2"], s["m2"], s["l2"]), merge(s))
+    def phase2_fused(s):  # this group's sources merged with (o1, m1, l1) and normalised in one pass
+        v = s["v"][split:n]
+        _lib.check(lib.sy_attn_with_stats_merge(P(v), P(w), P(s["o1"]), P(s["m1"]), P(s["l1"]), P(s["out"]),
+                                                P(s["mo"]), P(s["lo"]), n - split, nt, d, nt * d, code, code, 1e-6,
+                                                1, st), "sy_attn_with_stats_merge")
+
+    emit("two_phase_fwd", timed([lambda s=s: (stats_fwd(s, 0, split, s["o1"], s["m1"], s["l1"]), phase2_fused(s))
                                  for s in sets]), fw,
-         note=f"groups [0,{split}) and [{split},{n}) then the merge; bytes counted as the single pass's")
+         note=f"group [0,{split}) with statistics, then group [{split},{n}) merged with it and normalised in "
+              "one pass (2 kernels); bytes counted as the single pass's",
+         actual_bytes=(n + 3) * slab + 4 * nt * 4)
+    emit("two_phase_fwd_unfused", timed([lambda s=s: (stats_fwd(s, 0, split, s["o1"], s["m1"], s["l1"]),
+                                                      stats_fwd(s, split, n, s["o2"], s["m2"], s["l2"]), merge(s))
+                                         for s in sets]), fw,
+         note=f"groups [0,{split}) and [{split},{n}) then the merge kernel (3 kernels, o unnormalised); bytes "
+              "counted as the single pass's")
     del sets
     torch.cuda.empty_cache()
 

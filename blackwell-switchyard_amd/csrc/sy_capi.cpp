@@ -479,6 +479,43 @@ int sy_attn_with_stats(const void* v, const void* w, void* o, float* m, float* l
                   (hipStream_t)stream);
 }
 
+int sy_attn_with_stats_merge(const void* v, const void* w, const void* o1, const float* m1,
+                             const float* l1, void* out, float* m, float* l, int64_t n_src,
+                             int64_t n_tok, int64_t d, int64_t src_stride, int v_dtype,
+                             int w_dtype, float eps, int normalize, void* stream) {
+  if (n_tok != 0 && (v == nullptr || w == nullptr || o1 == nullptr || m1 == nullptr ||
+                     l1 == nullptr || out == nullptr || m == nullptr || l == nullptr))
+    return SY_ERR_NULL;
+  int rc = check_common(n_src, n_tok, d, src_stride, v_dtype, w_dtype);
+  if (rc != SY_OK) return rc;
+  if (normalize != 0 && normalize != 1) return SY_ERR_OP;
+  bool ok = false;
+  RowTable t = stacked(v, n_src, src_stride, v_dtype, &ok);
+  const hipStream_t s = (hipStream_t)stream;
+  // The prior's o1 rides in the register tile as row n_src: a resident tile
+  // of n_src + 1 rows, addressed through the table's row pointers.
+  const bool aligned = vec_rows(ok, d, v_dtype) && al16(w) && al16(out) && al16(o1);
+  sy_plan p;
+  rc = make_plan(SY_OP_FWD, n_src + 1, 0, d, v_dtype, w_dtype, aligned, &p);
+  if (rc != SY_OK) return rc;
+  apply_tile_rules(SY_OP_FWD, n_src + 1, n_tok, d, &p);
+  if (n_tok == 0) return SY_OK;
+  if (p.family == SY_FAMILY_RESIDENT && n_src + 1 <= kTableRows && p.rows_per_tile >= n_src + 1) {
+    t.p[n_src] = const_cast<void*>(o1);
+    FwdArgs a{t,      w,       out,     nullptr, m,  l,  normalize, (int)n_src,
+              n_tok,  (int)d,  v_dtype, w_dtype, eps, m1, l1};
+    return status(fwd_vec(p, a, s));
+  }
+  // Beyond the resident tiles (more rows, unaligned rows, mixed dtypes): this
+  // group's (o, m, l) into out, m, l, then the merge over them in place.
+  rc = fwd_impl(t, ok, w, out, nullptr, m, l, 0, n_src, n_tok, d, v_dtype, w_dtype, eps, s);
+  if (rc != SY_OK) return rc;
+  const bool vec = al16(o1) && al16(out) && (d * esize(v_dtype)) % 16 == 0;
+  MergeArgs ma{o1, m1, l1, out, m, l, out, m, l, n_tok, (int)d};
+  ma.normalize = normalize;
+  return status(launch_merge(ma, v_dtype, vec, s));
+}
+
 int sy_sol(const void* v, void* out, int64_t n_src, int64_t n_tok, int64_t d, int64_t src_stride,
            int dtype, void* stream) {
   if (n_tok != 0 && (v == nullptr || out == nullptr)) return SY_ERR_NULL;

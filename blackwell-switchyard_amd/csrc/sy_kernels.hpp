@@ -471,12 +471,23 @@ k_batched(const RowTable v, const typename T::storage* __restrict__ q,
 // extra registers. `n_iter` is the slot trip count of the busiest slot; slots
 // with fewer tokens re-read their last token and store nothing, so when W > 1
 // every wave of the workgroup meets the same barriers.
-template <class T, int W, int VPL, int NR>
+//
+// MERGE: phase 2 of the two-phase schedule in the same pass (reference
+// src/switchyard/reference.py:195-233, attn_with_stats then
+// merge_online_softmax). Row n_src of the table is a prior group's
+// unnormalised o1 (v's dtype), pm/pl its m1, l1 per token. It rides in the
+// tile as one more row, refilled like the sources, and enters the sum with
+// weight s1 = exp(m1 - M), M = max(m1, max_n logit_n):
+//     o = s1 o1 + sum_n exp(logit_n - M) v_n,   l = s1 l1 + sum_n exp(logit_n - M)
+// so the group's own o is never rounded or written (the merge kernel would
+// re-read it), and out is o / l (normalize) or o with (M, l).
+template <class T, int W, int VPL, int NR, bool MERGE = false>
 __global__ void __launch_bounds__(FwdGeom<W>::kBlock)
 k_fwd_res(const RowTable v, const typename T::storage* __restrict__ w,
           typename T::storage* __restrict__ out, float* __restrict__ stats,
           float* __restrict__ m_out, float* __restrict__ l_out, int normalize, int n_src,
-          int64_t n_tok, int d, float eps, float inv_d, int n_iter) {
+          int64_t n_tok, int d, float eps, float inv_d, int n_iter,
+          const float* __restrict__ pm = nullptr, const float* __restrict__ pl = nullptr) {
   using S = typename T::storage;
   constexpr int CE = T::ce;
   constexpr int TPB = FwdGeom<W>::kTpb;
@@ -497,7 +508,12 @@ k_fwd_res(const RowTable v, const typename T::storage* __restrict__ w,
   }
   const uint32_t row_bytes = (uint32_t)d * sizeof(S);
   const uint32_t lane_off = (uint32_t)(seg * 64 + lane) * 16u;
-  const int rows = n_src;  // host guarantees n_src <= NR
+  const int rows = n_src;  // host guarantees n_src <= NR (n_src + 1 with MERGE)
+  const int tile_rows = MERGE ? n_src + 1 : n_src;
+  // MERGE: lane 0 holds the token's m1, lane 1 its l1, fetched one token
+  // ahead by one vector load (a per-lane address, so no scalar-cache wait
+  // sits at the use).
+  const float* pstat_src = (lane & 1) ? pl : pm;
 
   i32x4_t wq[VPL];
   {
@@ -506,15 +522,19 @@ k_fwd_res(const RowTable v, const typename T::storage* __restrict__ w,
     for (int j = 0; j < VPL; ++j) wq[j] = ld16(wr, lane_off + j * kStep);
   }
   i32x4_t x[NR][VPL];
+  float pstat = 0.0f;
   {
     const int64_t t0 = first < n_tok ? first : n_tok - 1;
 #pragma unroll
     for (int n = 0; n < NR; ++n) {
-      if (n < opaque(rows)) {
+      if (n < opaque(tile_rows)) {
         const auto r = make_rsrc(row_of<const S>(v, n) + t0 * d, row_bytes);
 #pragma unroll
         for (int j = 0; j < VPL; ++j) x[n][j] = ld16_stream(r, lane_off + j * kStep);
       }
+    }
+    if constexpr (MERGE) {
+      if (lane < 2) pstat = pstat_src[t0];
     }
   }
 
@@ -523,6 +543,12 @@ k_fwd_res(const RowTable v, const typename T::storage* __restrict__ w,
     const bool live = tok < n_tok;
     const bool more = k + 1 < iters;
     const int64_t nxt = tok + slots < n_tok ? tok + slots : n_tok - 1;
+    float pm_tok = 0.0f, pl_tok = 0.0f;
+    if constexpr (MERGE) {
+      pm_tok = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pstat), 0));
+      pl_tok = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pstat), 1));
+      if (more && lane < 2) pstat = pstat_src[nxt];
+    }
 
     float part[2 * NR];
     if constexpr (NR <= 9) {
@@ -565,6 +591,7 @@ k_fwd_res(const RowTable v, const typename T::storage* __restrict__ w,
     float m = -INFINITY;
 #pragma unroll
     for (int n = 0; n < NR; ++n) {
+      if constexpr (MERGE) lg[n] = -INFINITY;  // the prior row's slot: weight s1
       if (n < opaque(rows)) {
         const float r = rsqrtf(fmaf(part[n], inv_d, eps));
         lg[n] = part[NR + n] * r;
@@ -578,11 +605,17 @@ k_fwd_res(const RowTable v, const typename T::storage* __restrict__ w,
 #pragma unroll
       for (int e = 0; e < CE; ++e) acc[j][e] = 0.0f;
     float l = 0.0f;
+    float s1 = 0.0f;
+    if constexpr (MERGE) {
+      m = fmaxf(m, pm_tok);
+      s1 = expf(pm_tok - m);
+    }
 #pragma unroll
     for (int n = 0; n < NR; ++n) {
-      if (n < opaque(rows)) {
-        const float p = expf(lg[n] - m);
-        l += p;
+      if (n < opaque(tile_rows)) {
+        const bool prior = MERGE && n == rows;
+        const float p = prior ? s1 : expf(lg[n] - m);
+        if (!prior) l += p;
 #pragma unroll
         for (int j = 0; j < VPL; ++j)
 #pragma unroll
@@ -594,6 +627,7 @@ k_fwd_res(const RowTable v, const typename T::storage* __restrict__ w,
         }
       }
     }
+    if constexpr (MERGE) l = fmaf(s1, pl_tok, l);
     if (live) {
       if (stats != nullptr && seg == 0) {
         // One store instruction for the token's 2N statistics (lane i < N the

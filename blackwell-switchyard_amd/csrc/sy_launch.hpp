@@ -125,6 +125,10 @@ struct FwdArgs {
   int v_dtype;
   int w_dtype;
   float eps;
+  // Phase 2 of the two-phase schedule (resident tiles only): row n_src of v
+  // is a prior group's o1, these its m1 and l1 [n_tok]; nullptr otherwise.
+  const float* prior_m = nullptr;
+  const float* prior_l = nullptr;
 };
 
 struct BwdArgs {
@@ -253,6 +257,7 @@ struct MergeArgs {
   float* l;
   int64_t n_tok;
   int d;
+  int normalize = 0;  // 1: o = merged o / merged l (the operator's output)
 };
 struct MergeBwdArgs {
   const void* o1;

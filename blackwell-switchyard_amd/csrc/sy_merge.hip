@@ -31,7 +31,8 @@ template <class T, bool VEC>
 __global__ void __launch_bounds__(kBlock)
 k_merge(const void* __restrict__ o1, const float* __restrict__ m1, const float* __restrict__ l1,
         const void* __restrict__ o2, const float* __restrict__ m2, const float* __restrict__ l2,
-        void* __restrict__ o, float* __restrict__ m, float* __restrict__ l, int64_t n_tok, int d) {
+        void* __restrict__ o, float* __restrict__ m, float* __restrict__ l, int64_t n_tok, int d,
+        int normalize) {
   using S = typename T::storage;
   constexpr int CE = T::ce;
   const int lane = threadIdx.x & 63;
@@ -39,7 +40,11 @@ k_merge(const void* __restrict__ o1, const float* __restrict__ m1, const float* 
   for (int64_t tok = (int64_t)blockIdx.x * kWaves + wave_id(); tok < n_tok; tok += stride) {
     const float a = m1[tok], b = m2[tok];
     const float mm = fmaxf(a, b);
-    const float s1 = expf(a - mm), s2 = expf(b - mm);
+    const float e1 = expf(a - mm), e2 = expf(b - mm);
+    const float ll = fmaf(e1, l1[tok], e2 * l2[tok]);
+    // normalize: the row weights carry 1 / l, so o / l costs no extra pass.
+    const float inv = normalize ? 1.0f / ll : 1.0f;
+    const float s1 = e1 * inv, s2 = e2 * inv;
     if constexpr (VEC) {
       const uint32_t row_bytes = (uint32_t)d * sizeof(S);
       const auto r1 = make_rsrc(static_cast<const S*>(o1) + tok * d, row_bytes);
@@ -72,7 +77,7 @@ k_merge(const void* __restrict__ o1, const float* __restrict__ m1, const float* 
     }
     if (lane == 0) {
       m[tok] = mm;
-      l[tok] = fmaf(s1, l1[tok], s2 * l2[tok]);
+      l[tok] = ll;
     }
   }
 }
@@ -165,10 +170,10 @@ hipError_t merge_t(const MergeArgs& a, bool vec, hipStream_t s) {
   const unsigned grid = merge_grid(a.n_tok);
   if (vec) {
     hipLaunchKernelGGL((k_merge<T, true>), dim3(grid), dim3(kBlock), 0, s, a.o1, a.m1, a.l1, a.o2,
-                       a.m2, a.l2, a.o, a.m, a.l, a.n_tok, a.d);
+                       a.m2, a.l2, a.o, a.m, a.l, a.n_tok, a.d, a.normalize);
   } else {
     hipLaunchKernelGGL((k_merge<T, false>), dim3(grid), dim3(kBlock), 0, s, a.o1, a.m1, a.l1, a.o2,
-                       a.m2, a.l2, a.o, a.m, a.l, a.n_tok, a.d);
+                       a.m2, a.l2, a.o, a.m, a.l, a.n_tok, a.d, a.normalize);
   }
   return hipGetLastError();
 }

@@ -96,6 +96,8 @@ SIGNATURES = {
                                       _i64, _i64, _i32, _i32, ctypes.c_float, _vp]),
     "sy_batched_with_stats": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32,
                                      ctypes.c_float, _vp]),
+    "sy_attn_with_stats_merge": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
+                                        _i32, _i32, ctypes.c_float, _i32, _vp]),
     "sy_merge_stats": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp]),
     "sy_merge_stats_bwd": (_i32, [_vp] * 15 + [_i64, _i64, _i32, _vp]),
     "sy_bwd_batched_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i32]),

@@ -13,6 +13,9 @@ and its batched API returns no statistics; here they are HIP operators:
 * ``merge_online_softmax(o1, m1, l1, o2, m2, l2)`` -> ``(o, m, l)``, with autograd;
 * ``block_attn_res_batched_with_stats(v, queries)`` -> ``(o, m, l)`` per query,
   one read of ``v`` for all queries (output only);
+* ``attn_with_stats_merge(v, w, o1, m1, l1)`` -> ``(out, m, l)``: phase 2 of
+  the schedule in one pass, this group's sources merged with a prior group's
+  triple before anything is written (normalised by default), with autograd;
 * ``block_attn_res_two_phase(v, w, split)`` composes them; it equals the
   single-pass operator up to rounding.
 
@@ -32,6 +35,7 @@ from .reference import DEFAULT_EPS
 __all__ = [
     "attn_with_stats",
     "merge_online_softmax",
+    "attn_with_stats_merge",
     "block_attn_res_batched_with_stats",
     "block_attn_res_two_phase",
 ]
@@ -162,6 +166,63 @@ def merge_online_softmax(o1, m1, l1, o2, m2, l2):
     return _MergeStats.apply(o1, m1, l1, o2, m2, l2)
 
 
+class _AttnWithStatsMerge(torch.autograd.Function):
+    """Forward: one launch of ``sy_attn_with_stats_merge``. Backward: the
+    gradient of the same function, evaluated through the two kernels it fuses
+    (``attn_with_stats`` of this group, then the merge and the division),
+    which recomputes this group's partial result once."""
+
+    @staticmethod
+    def forward(ctx, v, w, o1, m1, l1, eps: float, normalize: bool):
+        n, b, t, d = _validate(v, w)
+        _validate_triple(o1, m1, l1, "prior group")
+        if o1.shape != (b, t, d) or o1.dtype != v.dtype or o1.device != v.device:
+            raise ValueError(f"prior group: o1 must be [B, T, D] = {(b, t, d)} in v's dtype and device")
+        v, w, o1, m1, l1 = (x.contiguous() for x in (v, w, o1, m1, l1))
+        n_tok = b * t
+        out = torch.empty(b, t, d, device=v.device, dtype=v.dtype)
+        m = torch.empty(b, t, device=v.device, dtype=torch.float32)
+        ell = torch.empty(b, t, device=v.device, dtype=torch.float32)
+        if n_tok > 0 and d > 0:
+            with torch.cuda.device(v.device):
+                rc = _lib.lib().sy_attn_with_stats_merge(
+                    _ptr(v), _ptr(w), _ptr(o1), _ptr(m1), _ptr(l1), _ptr(out), _ptr(m), _ptr(ell), n, n_tok,
+                    d, n_tok * d, _lib.dtype_code(v.dtype), _lib.dtype_code(w.dtype), float(eps),
+                    int(bool(normalize)), _lib.stream_ptr(v.device),
+                )
+            _lib.check(rc, "sy_attn_with_stats_merge")
+        ctx.save_for_backward(v, w, o1, m1, l1)
+        ctx.eps = float(eps)
+        ctx.normalize = bool(normalize)
+        return out, m, ell
+
+    @staticmethod
+    def backward(ctx, gout, gm, gl):
+        v, w, o1, m1, l1 = ctx.saved_tensors
+        leaves = [x.detach().requires_grad_(need) for x, need in zip((v, w, o1, m1, l1), ctx.needs_input_grad)]
+        with torch.enable_grad():
+            o2, m2, l2 = attn_with_stats(leaves[0], leaves[1], ctx.eps)
+            o, m, ell = merge_online_softmax(leaves[2], leaves[3], leaves[4], o2, m2, l2)
+            out = (o.float() / ell.unsqueeze(-1)).to(v.dtype) if ctx.normalize else o
+            pairs = [(y, g) for y, g in ((out, gout), (m, gm), (ell, gl)) if g is not None]
+            wanted = [x for x in leaves if x.requires_grad]
+            grads = torch.autograd.grad([y for y, _ in pairs], wanted, [g for _, g in pairs], allow_unused=True)
+        it = iter(grads)
+        res = [next(it) if x.requires_grad else None for x in leaves]
+        return (*res, None, None)
+
+
+def attn_with_stats_merge(v: torch.Tensor, w: torch.Tensor, o1: torch.Tensor, m1: torch.Tensor, l1: torch.Tensor,
+                          eps: float = DEFAULT_EPS, normalize: bool = True):
+    """Phase 2 of the two-phase schedule (the paper's Algorithm 1, lines 10-12;
+    reference.py:194-233) in one pass: ``attn_with_stats(v, w)`` merged with a
+    prior group's ``(o1, m1, l1)`` by the online softmax before anything is
+    written. Returns ``(out, m, l)`` -- ``out`` is the operator's output over
+    both groups when ``normalize`` (the default), else the merged unnormalised
+    ``o``. Differentiable in every tensor argument."""
+    return _AttnWithStatsMerge.apply(v, w, o1, m1, l1, eps, normalize)
+
+
 def block_attn_res_batched_with_stats(v: torch.Tensor, queries: torch.Tensor, eps: float = DEFAULT_EPS):
     """``(o [S, B, T, D], m [S, B, T], l [S, B, T])``: ``attn_with_stats`` for
     ``S`` pseudo-queries sharing one read of ``v`` -- the batched inter-block
@@ -191,12 +252,13 @@ def block_attn_res_batched_with_stats(v: torch.Tensor, queries: torch.Tensor, ep
 
 
 def block_attn_res_two_phase(v: torch.Tensor, w: torch.Tensor, split: int, eps: float = DEFAULT_EPS):
-    """The two-phase schedule for one query: sources ``[0, split)`` and
-    ``[split, N)`` reduced separately, merged with the online softmax, then
-    normalised. Differentiable; equals ``block_attn_res_triton(v, w)`` up to
-    rounding (reference test_reference.py:139-150 states the exactness)."""
+    """The two-phase schedule for one query: sources ``[0, split)`` reduced to
+    their ``(o, m, l)``, then sources ``[split, N)`` reduced and merged with
+    them in one pass and normalised (two launches). Differentiable; equals
+    ``block_attn_res_triton(v, w)`` up to rounding (reference
+    test_reference.py:139-150 states the exactness)."""
     n = v.shape[0] if v.ndim == 4 else 0
     if not 0 < split < n:
         raise ValueError(f"split must be in (0, {n}), got {split}")
-    o, _, ell = merge_online_softmax(*attn_with_stats(v[:split], w, eps), *attn_with_stats(v[split:], w, eps))
-    return (o.float() / ell.unsqueeze(-1)).to(v.dtype)
+    out, _, _ = attn_with_stats_merge(v[split:], w, *attn_with_stats(v[:split], w, eps), eps=eps)
+    return out

@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define SY_ABI_VERSION 3
+#define SY_ABI_VERSION 4
 
 /* Most sources a per-source pointer list (the *_table entry points) may hold. */
 #define SY_MAX_TABLE_ROWS 16
@@ -141,6 +141,22 @@ int sy_fwd_table(const void* const* v_rows, const void* w, void* out, float* sta
 int sy_attn_with_stats(const void* v, const void* w, void* o, float* m, float* l, float* stats,
                        int64_t n_src, int64_t n_tok, int64_t d, int64_t src_stride, int v_dtype,
                        int w_dtype, float eps, void* stream);
+
+/* Phase 2 of the two-phase schedule in one pass: attn_with_stats over this
+ * group's sources merged with a prior group's (o1, m1, l1) before anything is
+ * written, so the group's own o is never stored and re-read:
+ *     M = max(m1, max_n logit_n),  s1 = exp(m1 - M),
+ *     o = s1 o1 + sum_n exp(logit_n - M) v_n,  l = s1 l1 + sum_n exp(logit_n - M).
+ * normalize = 1: out = o / l (the operator's output over both groups);
+ * normalize = 0: out = o, unnormalised, for a further merge. m and l always
+ * receive (M, l). o1 has v's dtype [n_tok][D]; m1, l1, m, l are fp32 [n_tok].
+ * Outputs must not overlap the prior's buffers. Replaces attn_with_stats
+ * followed by merge_online_softmax (src/switchyard/reference.py:194-233, the
+ * paper's Algorithm 1 phase 2, lines 10-12); SY_ERR_OP for normalize not 0/1. */
+int sy_attn_with_stats_merge(const void* v, const void* w, const void* o1, const float* m1,
+                             const float* l1, void* out, float* m, float* l, int64_t n_src,
+                             int64_t n_tok, int64_t d, int64_t src_stride, int v_dtype,
+                             int w_dtype, float eps, int normalize, void* stream);
 
 /* Merge two (o, m, l) results of disjoint source groups into their union:
  * m = max(m1, m2), s_i = exp(m_i - m), o = s1 o1 + s2 o2, l = s1 l1 + s2 l2.

@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_strings():
     lib = _lib.lib()
-    assert lib.sy_abi_version() == 3
+    assert lib.sy_abi_version() == 4
     for code in (OK, NULL, SHAPE, DTYPE, WORKSPACE, STRIDE, DEVICE, OP):
         assert lib.sy_strerror(code)
     assert b"NULL" in lib.sy_strerror(NULL)
@@ -132,6 +132,18 @@ def test_statistics_and_merge_entry_points_reject_bad_arguments():
     assert lib.sy_merge_stats(None, None, None, None, None, None, None, None, None, 0, 2048, BF16,
                               None) == OK
     assert lib.sy_merge_stats_bwd(*([f] * 14), None, 16, 2048, BF16, None) == NULL
+    # the fused phase 2: every pointer is required (m and l carry the merged
+    # statistics), normalize is 0 or 1, and nothing runs without tokens
+    assert lib.sy_attn_with_stats_merge(f, f, f, f, None, f, f, f, 5, 16, 2048, 16 * 2048, BF16, BF16,
+                                        1e-6, 1, None) == NULL
+    assert lib.sy_attn_with_stats_merge(f, f, f, f, f, f, None, f, 5, 16, 2048, 16 * 2048, BF16, BF16,
+                                        1e-6, 1, None) == NULL
+    assert lib.sy_attn_with_stats_merge(f, f, f, f, f, f, f, f, 5, 16, 2048, 100, BF16, BF16, 1e-6, 1,
+                                        None) == STRIDE
+    assert lib.sy_attn_with_stats_merge(f, f, f, f, f, f, f, f, 5, 16, 2048, 16 * 2048, BF16, BF16, 1e-6,
+                                        2, None) == OP
+    assert lib.sy_attn_with_stats_merge(None, None, None, None, None, None, None, None, 5, 0, 2048, 0, BF16,
+                                        BF16, 1e-6, 1, None) == OK
 
 
 def test_batched_backward_rejects_bad_arguments():
