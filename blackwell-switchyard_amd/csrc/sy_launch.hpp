@@ -39,7 +39,8 @@ constexpr int64_t kBwdBatchedMaxQ = 8;
 // Batched forward on the matrix cores (sy_matrix.hip): 16-bit inputs, at most
 // 16 sources and 16 queries (one MFMA tile each way), D in {512, 1024, 1536,
 // 2048} (four waves x 32-column MFMA steps; a wave keeps its query slice in
-// registers). Its stores address four query rows from one buffer resource, so
+// registers) and D = 4096 with N <= 9 (eight waves of 512 columns; the LDS
+// holds ten 8 KiB rows). Its stores address four query rows from one buffer resource, so
 // 4 * n_tok * D * 2 bytes must stay below 2^31 (else the per-query path runs).
 // Below kMatrixMinQ queries the register-tiled kernel is faster (config 3
 // shape, MI355X, register tile vs matrix cores: 2 queries 38.4 vs 50.0 us, 3:
@@ -50,7 +51,7 @@ constexpr int64_t kMatrixMinQ = 4;
 inline bool matrix_batched_fits(int64_t n_src, int64_t n_q, int64_t d, int dtype) {
   return (dtype == SY_BF16 || dtype == SY_F16) && n_src >= 1 && n_src <= kMatrixMaxRows &&
          n_q >= kMatrixMinQ && n_q <= kMatrixMaxQ &&
-         (d == 512 || d == 1024 || d == 1536 || d == 2048);
+         (d == 512 || d == 1024 || d == 1536 || d == 2048 || (d == 4096 && n_src <= 9));
 }
 inline bool matrix_batched_offsets_fit(int64_t n_q, int64_t n_tok, int64_t d) {
   return 4 * n_tok * d * 2 < ((int64_t)1 << 31) && n_q * n_tok * 4 < ((int64_t)1 << 31);

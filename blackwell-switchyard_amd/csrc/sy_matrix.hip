@@ -14,8 +14,9 @@
 // weights carry ~17 significant bits and the output keeps fp32-level error
 // before its single rounding.
 //
-// Work split: a workgroup of 4 waves owns one token at a time (persistent over
-// tokens); wave w owns the D/4 columns [w*D/4, (w+1)*D/4). Its slice of the
+// Work split: a workgroup of WV waves (4; 8 at D=4096) owns one token at a
+// time (persistent over tokens); wave w owns the D/WV columns [w*D/WV,
+// (w+1)*D/WV), at most 512, so a wave's registers are those of D=2048. Its slice of the
 // queries stays in registers for the whole kernel (B operand of the logits),
 // its slice of the token's rows goes to LDS, row-major, and is read twice: as
 // 16-byte row chunks for the logits and through ds_read_b64_tr_b16 (a 4x4
@@ -111,7 +112,7 @@ __device__ __forceinline__ void wave_lds_fence() {
 }
 
 // LDS: [n_src + 1][d * 2 + kMxPad] bytes of rows (the extra row is zero and
-// stands in for rows n >= n_src), then the exchange buffers. KS = D / 128
+// stands in for rows n >= n_src), then the exchange buffers. KS = D / (32 WV)
 // (32-column steps of a wave), NR >= n_src staged rows. Two tokens are in
 // flight per workgroup while a third is computed; the loop is unrolled by two
 // so that both staging sets keep compile-time register indices. The loads of a
@@ -123,20 +124,21 @@ __device__ __forceinline__ void wave_lds_fence() {
 // theirs), so the number of memory operations between a prefetch and its use
 // is a compile-time constant and the compiler waits for exactly the prefetch,
 // not for everything in flight.
-template <class T, int KS, int NR, int SQ, int TP>
-__global__ void __launch_bounds__(256 * TP, 2 / TP)
+template <class T, int KS, int NR, int SQ, int TP, int WV = kMxWaves>
+__global__ void __launch_bounds__(64 * WV * TP, 8 / (WV * TP))
 k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restrict__ out,
              float* __restrict__ m_out, float* __restrict__ l_out, int normalize, int n_src,
              int n_q, int64_t n_tok, float eps, float inv_d) {
   using M = Mx<T>;
-  constexpr int d = 128 * KS;
+  static_assert(WV * TP <= 8, "one workgroup of at most 8 waves per CU");
+  constexpr int d = 32 * KS * WV;
   constexpr uint32_t rs = (uint32_t)d * 2u + kMxPad;  // LDS row stride (bytes)
   constexpr uint32_t row_bytes = (uint32_t)d * 2u;
   constexpr int cpr = 4 * KS;  // 16-byte chunks per row in a wave's slice (<= 64)
   constexpr uint32_t kDrop = 0x80000000u;  // store offset past every resource
   extern __shared__ __align__(16) char vs_all[];
-  __shared__ __align__(16) float xl[2][TP][kMxWaves][64][4];  // logit partials, C layout
-  __shared__ __align__(16) float xs[2][TP][kMxWaves][kMxRows];  // sum-of-squares partials
+  __shared__ __align__(16) float xl[2][TP][WV][64][4];  // logit partials, C layout
+  __shared__ __align__(16) float xs[2][TP][WV][kMxRows];  // sum-of-squares partials
   // Output staging: [query][SC columns] per wave (the MFMA result layout
   // gives each lane 8 bytes of one query).
   // 256-column rounds halve the store count; the 16-row staging leaves no
@@ -147,14 +149,14 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
   constexpr int kLpq = SC / 8;                        // lanes per query row
   constexpr int kQpi = 64 / kLpq;                     // query rows per store
   constexpr int kRounds = SQ / kQpi;
-  __shared__ __align__(16) char ob[TP][kMxWaves][SQ * kRow];
+  __shared__ __align__(16) char ob[TP][WV][SQ * kRow];
 
   const int lane = threadIdx.x & 63;
-  // TP tokens per workgroup: waves 4h..4h+3 own token slot h (its own LDS
-  // rows and buffers); the slots of a workgroup advance in step (one barrier
-  // per token), so no co-resident slot runs ahead of another.
-  const int half = TP > 1 ? (int)(threadIdx.x >> 8) : 0;
-  const int w = (threadIdx.x >> 6) & 3;
+  // TP tokens per workgroup: waves WV*h .. WV*h + WV-1 own token slot h (its
+  // own LDS rows and buffers); the slots of a workgroup advance in step (one
+  // barrier per token), so no co-resident slot runs ahead of another.
+  const int half = TP > 1 ? (int)(threadIdx.x / (64 * WV)) : 0;
+  const int w = (threadIdx.x >> 6) % WV;
   char* const vs = vs_all + (size_t)half * (size_t)(n_src + 1) * rs;
   const int qi = lane & 15;  // MFMA column: query (logits, output) / row (A of logits)
   const int g = lane >> 4;   // 16-lane group
@@ -254,15 +256,15 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
     __syncthreads();
     mid();
     // Lane (g, qi) now holds rows n = 4g + j of query column s = qi.
-    f32x4_t pl4[kMxWaves], ps4[kMxWaves];
+    f32x4_t pl4[WV], ps4[WV];
 #pragma unroll
-    for (int ww = 0; ww < kMxWaves; ++ww) {
+    for (int ww = 0; ww < WV; ++ww) {
       pl4[ww] = *(const f32x4_t*)&xl[xb][half][ww][lane][0];
       ps4[ww] = *(const f32x4_t*)&xs[xb][half][ww][4 * g];
     }
     f32x4_t lt = pl4[0], sq = ps4[0];
 #pragma unroll
-    for (int ww = 1; ww < kMxWaves; ++ww) {
+    for (int ww = 1; ww < WV; ++ww) {
       lt += pl4[ww];
       sq += ps4[ww];
     }
@@ -853,10 +855,10 @@ k_bwd_batched_mx(const RowTable v, const uint16_t* __restrict__ q, const uint16_
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-template <class T, int KS, int NR, int SQ, int TP>
+template <class T, int KS, int NR, int SQ, int TP, int WV = kMxWaves>
 hipError_t launch_mx(const BatchedArgs& a, hipStream_t s, KernelRes* info) {
   const size_t lds = (size_t)TP * (size_t)(a.n_src + 1) * ((size_t)a.d * 2 + kMxPad);
-  auto* kern = k_batched_mx<T, KS, NR, SQ, TP>;
+  auto* kern = k_batched_mx<T, KS, NR, SQ, TP, WV>;
   KernelRes r{0, 0, 1, 0};
   // The attributes of an instantiation do not change: query them once.
   static hipFuncAttributes fa;
@@ -868,7 +870,7 @@ hipError_t launch_mx(const BatchedArgs& a, hipStream_t s, KernelRes* info) {
   r.lds = (int)(fa.sharedSizeBytes + lds);
   if (r.lds > 160 * 1024) return hipErrorInvalidConfiguration;
   const int alloc = std::max(8, ((fa.numRegs + 7) / 8) * 8);
-  const int by_waves = std::max(1, std::min(8, 512 / alloc) / TP);  // TP waves per SIMD
+  const int by_waves = std::max(1, std::min(8, 512 / alloc) / (WV * TP / 4));  // per SIMD
   r.blocks_per_cu = std::max(1, std::min(by_waves, (160 * 1024) / std::max(1, r.lds)));
   int cus = 0;
   if (cu_count(&cus) != hipSuccess || cus < 1) cus = 1;
@@ -883,7 +885,7 @@ hipError_t launch_mx(const BatchedArgs& a, hipStream_t s, KernelRes* info) {
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(kern, dim3(r.grid), dim3(64 * kMxWaves * TP), lds, s, a.v,
+  hipLaunchKernelGGL(kern, dim3(r.grid), dim3(64 * WV * TP), lds, s, a.v,
                      (const uint16_t*)a.q,
                      (uint16_t*)a.out, a.m_out, a.l_out, a.normalize, a.n_src, a.n_q, a.n_tok,
                      a.eps, 1.0f / (float)a.d);
@@ -930,6 +932,12 @@ hipError_t launch_mx_dtype(const BatchedArgs& a, hipStream_t s, KernelRes* info)
     case 8: return launch_mx_rows<T, 8>(a, s, info);
     case 12: return launch_mx_rows<T, 12>(a, s, info);
     case 16: return launch_mx_rows<T, 16>(a, s, info);
+    case 32:
+      // D = 4096: eight waves of 512 columns share a token (one workgroup per
+      // CU, N <= 9: ten 8 KiB LDS rows plus the exchange and staging buffers).
+      if (a.n_src > 9) return hipErrorInvalidConfiguration;
+      return a.n_q <= 8 ? launch_mx<T, 16, 9, 8, 1, 8>(a, s, info)
+                        : launch_mx<T, 16, 9, 16, 1, 8>(a, s, info);
     default: return hipErrorInvalidConfiguration;
   }
 }

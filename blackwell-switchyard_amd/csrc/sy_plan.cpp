@@ -144,11 +144,11 @@ int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_
 
   if (op == SY_OP_BATCHED && vec && matrix_batched_fits(n_src, n_q, d, v_dtype)) {
     out->family = SY_FAMILY_MATRIX;
-    out->waves_per_token = 4;
+    out->waves_per_token = d == 4096 ? 8 : 4;  // a wave's slice is at most 512 columns
     out->chunks_per_lane = 1;
     out->rows_per_tile = (int)kMatrixMaxRows;
     out->elems_per_chunk = ce;
-    out->block_threads = 256;
+    out->block_threads = 64 * out->waves_per_token;
     out->tokens_per_block = 1;
     out->n_chunks = 1;
     return SY_OK;

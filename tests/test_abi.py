@@ -253,7 +253,8 @@ def test_batched_query_cap():
 
 def test_batched_matrix_core_plan_bounds():
     """16-bit inputs with N <= 16, S <= 16 and D in {512, 1024, 1536, 2048}
-    take the matrix-core kernel; anything else keeps the register tiles."""
+    (and N <= 9 at D = 4096) take the matrix-core kernel; anything else keeps
+    the register tiles."""
     fam = lambda n, d, s, dt=torch.bfloat16: plan(_lib.OP_BATCHED, n, d, dt, n_q=s)["family_name"]
     for dt in (torch.bfloat16, torch.float16):
         for d in (512, 1024, 1536, 2048):
@@ -261,7 +262,12 @@ def test_batched_matrix_core_plan_bounds():
             assert fam(16, d, 16, dt) == "matrix"
     assert fam(9, 2048, 3) == "resident"  # few queries: the register tile is faster
     assert fam(17, 2048, 8) != "matrix"
-    assert fam(9, 4096, 8) == "resident"
+    # D = 4096: eight waves of 512 columns share a token, up to 9 rows
+    assert fam(9, 4096, 8) == "matrix" and fam(1, 4096, 16) == "matrix"
+    assert fam(10, 4096, 8) == "resident" and fam(9, 4096, 3) == "resident"
+    p4 = plan(_lib.OP_BATCHED, 9, 4096, n_q=8)
+    assert (p4["waves_per_token"], p4["block_threads"]) == (8, 512)
+    assert fam(9, 8192, 8) != "matrix"
     assert fam(9, 256, 8) == "resident"
     assert fam(9, 1000, 8) != "matrix"
     assert fam(9, 2048, 8, torch.float32) == "resident"

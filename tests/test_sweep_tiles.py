@@ -12,6 +12,7 @@ assertion fails before the numbers are compared.
 
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 
@@ -171,3 +172,71 @@ def test_query_sweep_shapes_at_the_oracle_floor(n_q, family, dtype):
     for i in range(n_q):
         err, floor = rel_l2(got[i], ref[i]), dtype_floor(ref[i], dtype)
         assert err <= 1.10 * floor, f"query {i}: rel_l2 {err:.4e} vs floor {floor:.4e}"
+
+
+#: The reference's eight-query shape checks of the batched forward
+#: (docs/batched_queries.md:27-34) as (N, B, T, D) and the family each
+#: launches on MI355X: the matrix cores everywhere, with eight waves of 512
+#: columns per token at D = 4096.
+EIGHT_QUERY_SHAPES = [((2, 1, 4096, 2048), "matrix"), ((16, 1, 4096, 2048), "matrix"),
+                      ((9, 1, 4096, 1024), "matrix"), ((9, 1, 128, 1024), "matrix"),
+                      ((9, 4, 2048, 2048), "matrix"), ((9, 1, 4096, 4096), "matrix")]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("shape,family", EIGHT_QUERY_SHAPES, ids=lambda x: str(x))
+def test_eight_query_shape_checks_at_the_oracle_floor(shape, family, dtype):
+    """Eight queries at each of the reference's shape checks, on the family the
+    sweep times, against the float64 C oracle at the 1.10x floor. Tokens are
+    independent, so the oracle runs on a slice of 256 tokens (the first and
+    last 128) of the full-size launch."""
+    from switchyard.triton_op import block_attn_res_batched
+
+    n, b, t, d = shape
+    n_q = 8
+    print(f"eight-query shape N{n} B{b} T{t} D{d} {dtype}", flush=True)
+    assert _lib.plan(_lib.OP_BATCHED, n, d, dtype, n_q=n_q)["family_name"] == family
+    gen = torch.Generator().manual_seed(n + t + d)
+    v = torch.randn(n, b, t, d, generator=gen).to(dtype)
+    q = (0.5 * torch.randn(n_q, d, generator=gen)).to(dtype)
+    got = block_attn_res_batched(v.to(DEV), q.to(DEV)).reshape(n_q, b * t, d).cpu()
+    flat = v.reshape(n, b * t, d)
+    pick = torch.cat([torch.arange(0, min(128, b * t)), torch.arange(max(128, b * t - 128), b * t)])
+    ref = torch.from_numpy(c_oracle.batched(flat[:, pick].double().numpy(), q.double().numpy()))
+    for i in range(n_q):
+        err, floor = rel_l2(got[i, pick], ref[i]), dtype_floor(ref[i], dtype)
+        assert err <= 1.10 * floor, f"query {i}: rel_l2 {err:.4e} vs floor {floor:.4e}"
+
+
+@pytest.mark.parametrize("t", [1, 3, 4 * CUS + 5])
+@pytest.mark.parametrize("n_q", [4, 16])
+def test_matrix_batched_forward_at_d4096_ragged(t, n_q):
+    """The eight-wave D = 4096 matrix-core tile at token counts below, at and
+    past the grid (an idle workgroup, a ragged last round), with 4 and 16
+    queries and 1-9 sources, including the statistics outputs."""
+    from switchyard.stats_op import block_attn_res_batched_with_stats
+    from switchyard.triton_op import block_attn_res_batched
+
+    d = 4096
+    for n in (1, 5, 9):
+        print(f"D=4096 matrix N{n} T{t} Q{n_q}", flush=True)
+        assert _lib.plan(_lib.OP_BATCHED, n, d, torch.bfloat16, n_q=n_q)["family_name"] == "matrix"
+        gen = torch.Generator().manual_seed(7 * n + t)
+        v = torch.randn(n, 1, t, d, generator=gen).to(torch.bfloat16)
+        q = (0.5 * torch.randn(n_q, d, generator=gen)).to(torch.bfloat16)
+        got = block_attn_res_batched(v.to(DEV), q.to(DEV)).reshape(n_q, t, d).cpu()
+        o, m, ell = block_attn_res_batched_with_stats(v.to(DEV), q.to(DEV))
+        ref = torch.from_numpy(c_oracle.batched(v.double()[:, 0].numpy(), q.double().numpy()))
+        v64 = v.double()[:, 0].numpy()
+        r = 1.0 / np.sqrt((v64**2).mean(-1) + 1e-6)  # [n, t]
+        for i in range(n_q):
+            assert rel_l2(got[i], ref[i]) <= 1.10 * dtype_floor(ref[i], torch.bfloat16), (n, i)
+            ro, rm, rl = c_oracle.attn_with_stats(v64, q[i].double().numpy())
+            assert rel_l2(o[i].reshape(t, d).cpu(), torch.from_numpy(ro)) <= 1.10 * dtype_floor(
+                torch.from_numpy(ro), torch.bfloat16), (n, i)
+            # m is a logit, a dot product over D that may cancel to far below
+            # its terms: 1e-5 relative plus 2**-20 of the terms' absolute sum
+            terms = ((np.abs(v64) @ np.abs(q[i].double().numpy())) * r).max(0)
+            dm = np.linalg.norm(m[i].reshape(t).cpu().double().numpy() - rm)
+            assert dm <= 1e-5 * np.linalg.norm(rm) + 2.0**-20 * np.linalg.norm(terms), (n, i)
+            assert rel_l2(ell[i].reshape(t).cpu(), torch.from_numpy(rl)) <= 1e-5
