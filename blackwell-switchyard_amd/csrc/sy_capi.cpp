@@ -92,11 +92,16 @@ int bwd_plan(int64_t n_src, int64_t n_tok, int64_t d, int v_dtype, int w_dtype, 
 }
 
 // Partial rows the backward's workspace provides: the largest persistent
-// grid of the vector plans (every variant, with and without forward stats).
-// A call whose buffers are not 16-byte aligned runs the generic kernel, which
-// is persistent over tokens at any grid and is capped to this count, so the
-// workspace is sized by the vector plans alone (2 MiB instead of 8 at N=9,
-// D=2048 on 256 CUs).
+// grid of the plans an aligned call takes (every variant, with and without
+// forward stats) -- vector tiles, and the generic kernel where an aligned
+// variant has no tile (17 <= N <= 32 without stats, over per-row pointers or
+// for the (o, m, l) gradient; every variant past 32 rows). A call whose buffers
+// are not 16-byte aligned also runs the generic kernel, which is persistent
+// over tokens at any grid and is capped to this count, so misalignment alone
+// does not widen the workspace (2 MiB instead of 8 at N=9, D=2048 on 256 CUs).
+// Capping the aligned generic variants to the 32-row tile's grid instead ran
+// them 3x slower (N=24 / N=32 at T=4096, D=2048, no stats, on MI355X: 3070 /
+// 4060 us on 256 workgroups against 976 / 1323 us on 1024).
 int workspace_rows(int64_t n_src, int64_t n_tok, int64_t d, int v_dtype, int w_dtype, int* rows) {
   int g = 0;
   for (bool st : {true, false}) {
@@ -104,19 +109,11 @@ int workspace_rows(int64_t n_src, int64_t n_tok, int64_t d, int v_dtype, int w_d
       sy_plan p;
       int rc = bwd_plan(n_src, n_tok, d, v_dtype, w_dtype, 1, st, var, &p);
       if (rc != SY_OK) return rc;
-      if (p.family == SY_FAMILY_GENERIC) continue;  // persistent at any grid: capped below
       int gi = 0;
       rc = bwd_grid(p, n_tok, v_dtype, st, var, &gi);
       if (rc != SY_OK) return rc;
       if (gi > g) g = gi;
     }
-  }
-  if (g == 0) {  // no vector plan at all: the generic kernel's own grid
-    sy_plan p;
-    int rc = make_plan(SY_OP_BWD, n_src, 0, d, v_dtype, w_dtype, 0, &p, true);
-    if (rc != SY_OK) return rc;
-    rc = bwd_grid(p, n_tok, v_dtype, true, 0, &g);
-    if (rc != SY_OK) return rc;
   }
   *rows = g;
   return SY_OK;
