@@ -75,6 +75,17 @@ hipError_t SY_FN(launch_fwd_vec_)(const sy_plan& p, const FwdArgs& a, hipStream_
                            a.prior_m, a.prior_l);                                            \
         return hipGetLastError();                                                            \
       }                                                                                      \
+      if constexpr (W_ == 1) {                                                               \
+        /* at most two tokens a wave: the final token in one pass (k_fwd_res, FIN) */        \
+        static const KernelRes kf = resources_of(k_fwd_res<T, W_, V_, N_, false, true>, kB); \
+        if (n_iter <= 2 && kf.blocks_per_cu >= kr.blocks_per_cu) {                           \
+          hipLaunchKernelGGL((k_fwd_res<T, W_, V_, N_, false, true>), dim3(grid), dim3(kB), 0, \
+                             s, a.v, (const St*)a.w, (St*)a.out, a.stats, a.m_out, a.l_out,  \
+                             a.normalize, a.n_src, a.n_tok, a.d, a.eps, inv_d, n_iter,       \
+                             nullptr, nullptr);                                              \
+          return hipGetLastError();                                                          \
+        }                                                                                    \
+      }                                                                                      \
       hipLaunchKernelGGL((k_fwd_res<T, W_, V_, N_>), dim3(grid), dim3(kB), 0, s, a.v,        \
                          (const St*)a.w, (St*)a.out, a.stats, a.m_out, a.l_out, a.normalize, \
                          a.n_src, a.n_tok, a.d, a.eps, inv_d, n_iter, nullptr, nullptr);     \

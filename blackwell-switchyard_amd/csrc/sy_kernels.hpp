@@ -481,7 +481,22 @@ k_batched(const RowTable v, const typename T::storage* __restrict__ q,
 //     o = s1 o1 + sum_n exp(logit_n - M) v_n,   l = s1 l1 + sum_n exp(logit_n - M)
 // so the group's own o is never rounded or written (the merge kernel would
 // re-read it), and out is o / l (normalize) or o with (M, l).
-template <class T, int W, int VPL, int NR, bool MERGE = false>
+//
+// FIN (one wave per token, no MERGE): a wave's final token, whose rows have
+// no later loads to overlap, folds each row in as soon as it lands instead of
+// waiting for all rows before the softmax: per-row sums (one two-value
+// transposed sum), weights exp(logit_n - logit_0) relative to row 0's logit
+// (acc and l rescaled if a later row's logit exceeds the reference by 32, so
+// no weight exceeds e^32), and the reference folded out at the end (o / l is
+// invariant to it; m_out, l_out and an unnormalised o are taken relative to
+// the max). Only the last row's work then follows the last load. Launched for
+// at most two tokens per wave: config 2's forward 29.5 -> 29.0 us, T = 2048
+// 16.7 -> 16.4, T = 1024 11.2 -> 10.9 (MI355X, same kernel otherwise); with
+// four or more tokens per wave the variant's loop ran 0.3-0.4 us a token
+// slower (T = 8192: 56.1 vs 56.5; T = 16384: 111.9 vs 113.3). A final token's
+// weights carry a different rounding than the two-pass form's, so a token's
+// bits depend on whether it is its wave's last (both within one rounding).
+template <class T, int W, int VPL, int NR, bool MERGE = false, bool FIN = false>
 __global__ void __launch_bounds__(FwdGeom<W>::kBlock)
 k_fwd_res(const RowTable v, const typename T::storage* __restrict__ w,
           typename T::storage* __restrict__ out, float* __restrict__ stats,
@@ -548,6 +563,78 @@ k_fwd_res(const RowTable v, const typename T::storage* __restrict__ w,
       pm_tok = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pstat), 0));
       pl_tok = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pstat), 1));
       if (more && lane < 2) pstat = pstat_src[nxt];
+    }
+    if constexpr (FIN) {
+      static_assert(W == 1 && !MERGE, "the one-pass final token is for one-wave tokens without a prior");
+      if (!more) {
+        float acc[VPL][CE];
+#pragma unroll
+        for (int j = 0; j < VPL; ++j)
+#pragma unroll
+          for (int e = 0; e < CE; ++e) acc[j][e] = 0.0f;
+        float lg[NR], rr[NR];
+        float mref = 0.0f, l = 0.0f, m = -INFINITY;
+#pragma unroll
+        for (int n = 0; n < NR; ++n) {
+          if (n < opaque(rows)) {
+            float ss = 0.0f, dt = 0.0f;
+#pragma unroll
+            for (int j = 0; j < VPL; ++j) {
+              ss = dot<T>(x[n][j], x[n][j], ss);
+              dt = dot<T>(x[n][j], wq[j], dt);
+            }
+            const float pv[2] = {ss, dt};
+            const float s2 = tsum<2>(pv, lane);  // lanes 0..31: ss, 32..63: dt
+            const float ssum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s2), 0));
+            const float dsum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s2), 32));
+            rr[n] = rsqrtf(fmaf(ssum, inv_d, eps));
+            lg[n] = dsum * rr[n];
+            m = fmaxf(m, lg[n]);
+            if (n == 0) {
+              mref = lg[n];
+            } else if (lg[n] > mref + 32.0f) {
+              const float sc = expf(mref - lg[n]);
+              l *= sc;
+#pragma unroll
+              for (int j = 0; j < VPL; ++j)
+#pragma unroll
+                for (int e = 0; e < CE; ++e) acc[j][e] *= sc;
+              mref = lg[n];
+            }
+            const float p = expf(lg[n] - mref);
+            l += p;
+#pragma unroll
+            for (int j = 0; j < VPL; ++j)
+#pragma unroll
+              for (int e = 0; e < CE; ++e) acc[j][e] = fmaf(p, elem<T>(x[n][j], e), acc[j][e]);
+          }
+        }
+        const float adj = expf(mref - m);  // from the reference to the max
+        if (stats != nullptr) {
+          float sv = 0.0f;
+#pragma unroll
+          for (int n = 0; n < NR; ++n) {
+            sv = lane == n ? lg[n] : sv;
+            sv = lane == 32 + n ? rr[n] : sv;
+          }
+          const int i = lane & 31;
+          if (i < rows) stats[(int64_t)((lane >> 5) * n_src + i) * n_tok + tok] = sv;
+        }
+        if (m_out != nullptr && lane == 0) {
+          m_out[tok] = m;
+          l_out[tok] = l * adj;
+        }
+        const float inv_l = normalize ? 1.0f / l : adj;
+        const auto orr = make_rsrc(out + tok * d, row_bytes);
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+          float f[CE];
+#pragma unroll
+          for (int e = 0; e < CE; ++e) f[e] = acc[j][e] * inv_l;
+          st16_stream(orr, lane_off + j * kStep, pack<T>(f));
+        }
+        break;
+      }
     }
 
     float part[2 * NR];
