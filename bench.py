@@ -442,7 +442,7 @@ def _traffic_kernels(args):
                 ("merge_fwd", "k_merge", "k_merge_bwd", 3 * slab + 6 * 4096 * 4, wl),
                 ("merge_bwd", "k_merge_bwd", None, 5 * slab + 10 * 4096 * 4, wl),
                 # the fused phase 2 (5 sources + the prior's o1 in, out written)
-                ("phase2_fused", "4, 9, true>", None, 7 * slab + 4 * 4096 * 4, wl),
+                ("phase2_fused", "4, 9, true, false>", None, 7 * slab + 4 * 4096 * 4, wl),
                 ("table_bwd", "true, 1>", None, (2 * n + 1) * slab, wl)]
     if args.traffic_set in ("n4", "n16"):  # bench.py --sweep --sweep-only N4 (N16) --quick
         n, d = int(args.traffic_set[1:]), 2048
