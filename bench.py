@@ -712,7 +712,9 @@ def batched_sweep(args, results, failed):
 
         for s in sets:  # warm-up: first launches load code objects and query attributes
             batched(s)
-        iters = 3 if args.quick else max(20, min(100, int(2e5 / ((n + q) * nt * d / 1e4))))
+        # 100-call loops, as the config-3 line always used: 20-call loops of the
+        # batched forward read 5-8% slower (clocks still ramping between loops)
+        iters = 3 if args.quick else 100
         loop = harness.time_loop if args.quick else harness.time_loop_median
         ms = loop([lambda s=s: batched(s) for s in sets], device=dev, iters=iters)
         nbytes = attn_res_batched_bytes(n, q, b, t, d, item)
