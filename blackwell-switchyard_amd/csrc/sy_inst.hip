@@ -69,6 +69,16 @@ hipError_t SY_FN(launch_fwd_vec_)(const sy_plan& p, const FwdArgs& a, hipStream_
       const int n_iter = (int)cdiv(a.n_tok, (int64_t)grid * kT);                             \
       if (a.prior_m != nullptr) {                                                            \
         if (a.n_src + 1 > N_) return hipErrorInvalidConfiguration;                           \
+        if constexpr (W_ == 1) {                                                             \
+          static const KernelRes km = resources_of(k_fwd_res<T, W_, V_, N_, true, true>, kB); \
+          if (n_iter <= 2 && km.blocks_per_cu >= kr.blocks_per_cu) {                         \
+            hipLaunchKernelGGL((k_fwd_res<T, W_, V_, N_, true, true>), dim3(grid), dim3(kB), \
+                               0, s, a.v, (const St*)a.w, (St*)a.out, a.stats, a.m_out,      \
+                               a.l_out, a.normalize, a.n_src, a.n_tok, a.d, a.eps, inv_d,    \
+                               n_iter, a.prior_m, a.prior_l);                                \
+            return hipGetLastError();                                                        \
+          }                                                                                  \
+        }                                                                                    \
         hipLaunchKernelGGL((k_fwd_res<T, W_, V_, N_, true>), dim3(grid), dim3(kB), 0, s, a.v, \
                            (const St*)a.w, (St*)a.out, a.stats, a.m_out, a.l_out,            \
                            a.normalize, a.n_src, a.n_tok, a.d, a.eps, inv_d, n_iter,         \

@@ -482,12 +482,14 @@ k_batched(const RowTable v, const typename T::storage* __restrict__ q,
 // so the group's own o is never rounded or written (the merge kernel would
 // re-read it), and out is o / l (normalize) or o with (M, l).
 //
-// FIN (one wave per token, no MERGE): a wave's final token, whose rows have
+// FIN (one wave per token): a wave's final token, whose rows have
 // no later loads to overlap, folds each row in as soon as it lands instead of
 // waiting for all rows before the softmax: per-row sums (one two-value
 // transposed sum), weights exp(logit_n - logit_0) relative to row 0's logit
-// (acc and l rescaled if a later row's logit exceeds the reference by 32, so
-// no weight exceeds e^32), and the reference folded out at the end (o / l is
+// (with MERGE, relative to the prior's m1, the prior entering with weight 1
+// and its l1; acc and l rescaled if a later row's logit exceeds the
+// reference by 32, so no weight exceeds e^32), and the reference folded out
+// at the end (o / l is
 // invariant to it; m_out, l_out and an unnormalised o are taken relative to
 // the max). Only the last row's work then follows the last load. Launched for
 // at most two tokens per wave: config 2's forward 29.5 -> 29.0 us, T = 2048
@@ -565,7 +567,7 @@ k_fwd_res(const RowTable v, const typename T::storage* __restrict__ w,
       if (more && lane < 2) pstat = pstat_src[nxt];
     }
     if constexpr (FIN) {
-      static_assert(W == 1 && !MERGE, "the one-pass final token is for one-wave tokens without a prior");
+      static_assert(W == 1, "the one-pass final token is for one-wave tokens");
       if (!more) {
         float acc[VPL][CE];
 #pragma unroll
@@ -573,36 +575,44 @@ k_fwd_res(const RowTable v, const typename T::storage* __restrict__ w,
 #pragma unroll
           for (int e = 0; e < CE; ++e) acc[j][e] = 0.0f;
         float lg[NR], rr[NR];
-        float mref = 0.0f, l = 0.0f, m = -INFINITY;
+        // Reference logit: row 0's, or with MERGE the prior's m1, which is
+        // known before any row lands (the prior then enters with weight 1
+        // and its l1).
+        float mref = MERGE ? pm_tok : 0.0f, l = 0.0f, m = MERGE ? pm_tok : -INFINITY;
 #pragma unroll
         for (int n = 0; n < NR; ++n) {
-          if (n < opaque(rows)) {
-            float ss = 0.0f, dt = 0.0f;
+          if (n < opaque(tile_rows)) {
+            const bool prior = MERGE && n == rows;
+            float lgn = pm_tok;
+            if (!prior) {
+              float ss = 0.0f, dt = 0.0f;
 #pragma unroll
-            for (int j = 0; j < VPL; ++j) {
-              ss = dot<T>(x[n][j], x[n][j], ss);
-              dt = dot<T>(x[n][j], wq[j], dt);
+              for (int j = 0; j < VPL; ++j) {
+                ss = dot<T>(x[n][j], x[n][j], ss);
+                dt = dot<T>(x[n][j], wq[j], dt);
+              }
+              const float pv[2] = {ss, dt};
+              const float s2 = tsum<2>(pv, lane);  // lanes 0..31: ss, 32..63: dt
+              const float ssum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s2), 0));
+              const float dsum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s2), 32));
+              rr[n] = rsqrtf(fmaf(ssum, inv_d, eps));
+              lg[n] = dsum * rr[n];
+              lgn = lg[n];
+              m = fmaxf(m, lgn);
             }
-            const float pv[2] = {ss, dt};
-            const float s2 = tsum<2>(pv, lane);  // lanes 0..31: ss, 32..63: dt
-            const float ssum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s2), 0));
-            const float dsum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s2), 32));
-            rr[n] = rsqrtf(fmaf(ssum, inv_d, eps));
-            lg[n] = dsum * rr[n];
-            m = fmaxf(m, lg[n]);
-            if (n == 0) {
-              mref = lg[n];
-            } else if (lg[n] > mref + 32.0f) {
-              const float sc = expf(mref - lg[n]);
+            if (!MERGE && n == 0) {
+              mref = lgn;
+            } else if (lgn > mref + 32.0f) {
+              const float sc = expf(mref - lgn);
               l *= sc;
 #pragma unroll
               for (int j = 0; j < VPL; ++j)
 #pragma unroll
                 for (int e = 0; e < CE; ++e) acc[j][e] *= sc;
-              mref = lg[n];
+              mref = lgn;
             }
-            const float p = expf(lg[n] - mref);
-            l += p;
+            const float p = expf(lgn - mref);
+            l = prior ? fmaf(p, pl_tok, l) : l + p;
 #pragma unroll
             for (int j = 0; j < VPL; ++j)
 #pragma unroll
