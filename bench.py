@@ -1082,8 +1082,8 @@ def main() -> None:
     # 88.4 us at config 2 with 200 or 1000 warm-up steps).
     k_iters = max(args.steps, 200)
     per = {}
-    for name in ("fwd", "bwd_main", "bwd", "sol"):
-        per[name] = harness.time_loop(wl.closures(name), device=dev, iters=k_iters)
+    for name in ("fwd", "bwd_main", "bwd", "sol"):  # median of three loops after an untimed one
+        per[name] = harness.time_loop_median(wl.closures(name), device=dev, iters=k_iters)
     # The 4 us reduction alone is launch-bound in a host loop (each launch
     # costs the host more than the kernel takes): its share of the step is
     # timed as sy_bwd (main + reduction) minus the main kernel.
