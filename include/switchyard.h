@@ -121,7 +121,11 @@ int sy_plan_for_tokens(int op, int64_t n_src, int64_t n_q, int64_t n_tok, int64_
  * launches (src/switchyard/triton_op.py:505-536, :50-117).
  * `stats` may be NULL; when given it receives [2][N][n_tok] fp32: the logits,
  * then the inverse RMS r_n, which sy_bwd can reuse instead of recomputing.
- * w may have a different dtype from v (it is upcast, as in triton_op.py:67). */
+ * w may have a different dtype from v (it is upcast, as in triton_op.py:67).
+ * The same call on the same inputs returns the same bits. A token's result is
+ * rounded once either way, but its last bit can depend on the launch it is
+ * in (the tile the token count selects, and whether the persistent kernel
+ * takes it as a wave's final token, whose rows are folded in as they land). */
 int sy_fwd(const void* v, const void* w, void* out, float* stats, int64_t n_src, int64_t n_tok,
            int64_t d, int64_t src_stride, int v_dtype, int w_dtype, float eps, void* stream);
 
