@@ -266,22 +266,42 @@ void apply_tile_override(int op, int64_t n_src, int64_t d, sy_plan* p) {
 // forward + backward, us, plan tiles -> this rule):
 //   N=9  T=512: 9.41 -> 8.75,  25.0 -> 21.9     N=9  T=256: 8.95 -> 7.57, 23.7 -> 20.0
 //   N=4  T=512: 5.65 -> 5.07,  15.7 -> 14.1     N=16 T=512: 14.7 -> 13.6, 36.9 -> 32.7
-// At four tokens per CU (T = 1024) the one-wave tiles are faster again, and
-// N <= 2 gains nothing. Only 16-bit rows of four chunks a lane (W * VPL = 4)
-// were measured, so only those change. The forward takes (4,1) at up to one
-// token per CU, else (2,2); the backward (4,1).
+// At four tokens per CU (T = 1024) the one-wave tiles are faster again. The
+// forward takes (4,1) at up to one token per CU, else (2,2); the backward
+// (4,1), also at N = 2 (backward main kernel, device time from graph replays:
+// T=256 5.20 -> 3.91 us, T=512 5.73 -> 4.73; the forward gains nothing there).
+// Rows of two chunks a lane at one wave (16-bit D = 1024): the backward takes
+// (4,1) up to two tokens per CU and (2,1) at up to four. (4,1) covers twice the
+// row, and its upper two waves' loads, stores and partial-row writes fall
+// outside their buffer ranges, but it puts one token in each workgroup where
+// (2,1) puts two, so the tokens reach twice the CUs. Backward main kernel, us:
+//   N=9  T=128: 9.56 -> 6.94   T=512: 10.39 -> 7.67   T=1024: 10.93 -> 9.38
+//   N=16 T=128: 16.62 -> 11.54 T=512: 17.45 -> 12.35  T=1024: 18.23 -> 15.59
+//   N=2  T=512: 5.03 -> 3.91   N=4 T=512: 6.42 -> 4.93 (fp16 N=9 T=512: 10.35 -> 7.73)
+// and at eight tokens per CU the one-wave tile stays (N=16 T=2048: 26.1 vs 31.6).
+// The forward's one-wave tiles at D = 1024 are already the fastest there.
+// fp32 rows (four elements a chunk) behave the same in the backward: D = 1024
+// (four chunks a lane) N=9 T=128 9.75 -> 7.52, T=512 11.24 -> 9.19, N=16
+// T=128 16.65 -> 12.67, N=4 T=256 5.81 -> 4.49 (four tokens per CU: within
+// 4% either way, so the plan's tile); D = 512 (two chunks) N=9 T=256
+// 8.92 -> 7.25, T=1024 10.70 -> 9.33. The fp32 forward was not measured and
+// keeps its tiles.
 void apply_token_rule(int op, int64_t n_src, int64_t n_tok, sy_plan* p) {
   if (op != SY_OP_FWD && op != SY_OP_BWD) return;
   const bool tiled = p->family == SY_FAMILY_RESIDENT || p->family == SY_FAMILY_CHUNKED;
-  if (!tiled || n_src < 3 || n_src > 16 || p->elems_per_chunk != 8) return;
-  if (p->waves_per_token * p->chunks_per_lane != 4) return;
+  const bool bwd = op == SY_OP_BWD;
+  if (!tiled || n_src < 2 || n_src > 16) return;
+  if (!bwd && (p->elems_per_chunk != 8 || n_src < 3)) return;  // forward: 16-bit rows, N >= 3
+  const int span = p->waves_per_token * p->chunks_per_lane;  // one wave's chunks a lane
+  if (span != 4 && !(span == 2 && bwd && p->waves_per_token == 1)) return;
   int cus = 0;
   if (cu_count(&cus) != hipSuccess || cus < 1) return;
-  if (n_tok < 1 || n_tok > 2 * (int64_t)cus) return;
+  if (n_tok < 1 || n_tok > (span == 4 ? 2 : 4) * (int64_t)cus) return;
   const int nr = n_src <= 4 ? 4 : n_src <= 9 ? 9 : 16;
-  const int w = op == SY_OP_BWD || n_tok <= cus ? 4 : 2;
-  if (!tile_listed(op, w, 4 / w, nr)) return;
-  set(p, SY_FAMILY_RESIDENT, w, 4 / w, nr, p->elems_per_chunk, op, n_src);
+  const int w = span == 2 ? (n_tok <= 2 * (int64_t)cus ? 4 : 2) : (bwd || n_tok <= cus ? 4 : 2);
+  const int vpl = span == 2 ? 1 : 4 / w;
+  if (!tile_listed(op, w, vpl, nr)) return;
+  set(p, SY_FAMILY_RESIDENT, w, vpl, nr, p->elems_per_chunk, op, n_src);
 }
 
 void apply_tile_rules(int op, int64_t n_src, int64_t n_tok, int64_t d, sy_plan* p) {

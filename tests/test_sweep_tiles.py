@@ -74,8 +74,8 @@ SWEEP_CASES = [
     # N between the sweep points: the 16-row backward with a partly filled tile
     ((12, 1, 4 * 256, 2048), ("chunked", (1, 4, 4)), (1, 4, 16)),
     # D sweep tiles (config 4 uses B=4 T=4096; the tile depends only on the
-    # token count being above two per CU)
-    ((9, 4, 256, 1024), ("resident", (1, 2, 9)), (1, 2, 9)),
+    # token count being above two per CU, four for the D=1024 backward)
+    ((9, 4, 512, 1024), ("resident", (1, 2, 9)), (1, 2, 9)),
     ((9, 4, 256, 4096), ("resident", (2, 4, 9)), (2, 4, 9)),
     # 16 < N <= 32: the 32-row backward tile (the reference's n-sweep has N=32)
     ((32, 1, 4096, 2048), ("chunked", (1, 4, 4)), (2, 2, 32)),
