@@ -423,6 +423,25 @@ def _copy_probe_calibration(torch, dev) -> None:
     torch.cuda.synchronize(dev)
 
 
+def _launch_floor_and_copy_rate(torch, dev, loop, side) -> tuple[float, float]:
+    """The two floors a small shape's step is reported against: microseconds
+    per kernel of back-to-back launches of a kernel that does next to nothing
+    (the write probe on 16 bytes, one workgroup), replayed from a HIP graph so
+    that no host time is in it, and the 1 GiB copy probe's read+write rate in
+    GB/s."""
+    from switchyard import harness
+    from switchyard.hip_op import bandwidth_probe
+
+    tiny = torch.empty(4, dtype=torch.int32, device=dev)
+    floor_ms = harness.time_graph([lambda: bandwidth_probe("write", None, tiny)], stream=side, per_graph=200)
+    nbytes = 1 << 30
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(3)
+    dst = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    copy_ms = loop([lambda: bandwidth_probe("copy", src, dst)], device=dev, iters=20)
+    del src, dst
+    return floor_ms * 1e3, 2 * nbytes / copy_ms / 1e6
+
+
 def _traffic_kernels(args):
     """(label, name substring, excluded substring, algorithmic bytes per launch,
     workload) of the kernels a counter run of --traffic-set covered."""
@@ -579,6 +598,13 @@ def sweep_mode(args):
     results = []
     failed = []
     only = set(args.sweep_only.split(",")) if args.sweep_only else None
+    loop = harness.time_loop if args.quick else harness.time_loop_median
+    side = torch.cuda.Stream(dev)  # graph captures (device-only times)
+    side_ptr = ctypes.c_void_p(side.cuda_stream)
+    floor_us = copy_gbps = None  # --quick runs are counter targets: no extra probe launches
+    if not args.quick:
+        floor_us, copy_gbps = _launch_floor_and_copy_rate(torch, dev, loop, side)
+        log(f"launch floor {floor_us:.2f} us a kernel, copy probe {copy_gbps:.0f} GB/s")
     for (n, b, t, d), names in _sweep_shapes(only):
         name = names[0]
         nt = b * t
@@ -595,26 +621,50 @@ def sweep_mode(args):
         ws_bytes = int(lib.sy_bwd_workspace_bytes(n, nt, d, code, code))
         ws = torch.empty(max(1, ws_bytes // 4), device=dev)
 
-        def fwd(s):
+        def fwd(s, stream=st):
             _lib.check(lib.sy_fwd(P(s["v"]), P(w), P(s["out"]), P(s["stats"]), n, nt, d, nt * d, code, code,
-                                  1e-6, st), "sy_fwd")
+                                  1e-6, stream), "sy_fwd")
 
-        def bwd(s):
+        def bwd(s, stream=st):
             _lib.check(lib.sy_bwd(P(s["v"]), P(w), P(s["g"]), P(s["stats"]), P(s["dv"]), P(s["dw"]), P(ws),
-                                  ws_bytes, n, nt, d, nt * d, code, code, 1e-6, st), "sy_bwd")
+                                  ws_bytes, n, nt, d, nt * d, code, code, 1e-6, stream), "sy_bwd")
 
         def sol(s):  # the ceiling: same bytes and launch shape, out = sum_n v_n
             _lib.check(lib.sy_sol(P(s["v"]), P(s["out"]), n, nt, d, nt * d, code, st), "sy_sol")
 
         iters = max(20, min(200, int(2e5 / (n * t * b * d / 1e4))))
+        rows = int(lib.sy_bwd_partial_rows(n, nt, d, code, code, 1, 1))
+
+        def bwd_main(s, stream=st):  # sy_bwd's first kernel: dv and the dw partial rows
+            _lib.check(lib.sy_bwd_main(P(s["v"]), P(w), P(s["g"]), P(s["stats"]), P(s["dv"]), P(ws), ws_bytes,
+                                       n, nt, d, nt * d, code, code, 1e-6, stream), "sy_bwd_main")
+
+        def reduce(s, stream=st):  # its second: the partial rows summed into dw
+            _lib.check(lib.sy_dw_reduce(P(ws), rows, d, P(s["dw"]), code, stream), "sy_dw_reduce")
+
         for s in sets:  # warm-up: a shape's first launches query kernel attributes
             fwd(s)
             bwd(s)
-        loop = harness.time_loop if args.quick else harness.time_loop_median
         if args.quick:
             iters = 3
         f_ms = loop([lambda s=s: fwd(s) for s in sets], device=dev, iters=iters)
         fb_ms = loop([lambda s=s: (fwd(s), bwd(s)) for s in sets], device=dev, iters=iters)
+        fbg_ms = fg_ms = bm_ms = red_ms = None
+        if not args.quick:  # replayed from HIP graphs: device time only
+            fbg_ms = harness.time_graph([lambda s=s: (fwd(s, side_ptr), bwd(s, side_ptr)) for s in sets],
+                                        stream=side)
+            torch.cuda.synchronize(dev)
+            replayed = [sets[0][k].clone() for k in ("out", "dv", "dw")]
+            fwd(sets[0])
+            bwd(sets[0])
+            torch.cuda.synchronize(dev)
+            if not all(torch.equal(a, sets[0][k]) for a, k in zip(replayed, ("out", "dv", "dw"))):
+                failed.append(f"N{n} B{b} T{t} D{d} (graph replay differs from the eager step)")
+            # The split (dw is then the last set's: the partial rows are shared;
+            # the float64 gate below recomputes set 0 first).
+            fg_ms = harness.time_graph([lambda s=s: fwd(s, side_ptr) for s in sets], stream=side)
+            bm_ms = harness.time_graph([lambda s=s: bwd_main(s, side_ptr) for s in sets], stream=side)
+            red_ms = harness.time_graph([lambda s=s: reduce(s, side_ptr) for s in sets], stream=side)
         for s in sets:
             sol(s)
         sol_ms = loop([lambda s=s: sol(s) for s in sets], device=dev, iters=iters)
@@ -641,6 +691,13 @@ def sweep_mode(args):
                "fwd_pct_of_ceiling": round(100 * sol_ms / f_ms, 1),
                "fwd_bwd_us": round(fb_ms * 1e3, 2), "fwd_bwd_gbps": round(fb / fb_ms / 1e6, 1),
                "fwd_bwd_frac_hbm_peak": round(fb / fb_ms / 1e6 / HBM_PEAK_GBPS, 4),
+               "bwd_main_graph_us": None if bm_ms is None else round(bm_ms * 1e3, 2),
+               "reduce_graph_us": None if red_ms is None else round(red_ms * 1e3, 2),
+               # fwd+bwd's floor: its three kernels' launches plus its bytes at the copy rate
+               "fwd_graph_us": None if fg_ms is None else round(fg_ms * 1e3, 2),
+               "fwd_bwd_graph_us": None if fbg_ms is None else round(fbg_ms * 1e3, 2),
+               "launch_floor_us": None if floor_us is None else round(floor_us, 2),
+               "fwd_bwd_floor_us": None if floor_us is None else round(3 * floor_us + fb / copy_gbps / 1e3, 2),
                "workspace_bytes": ws_bytes + 2 * n * nt * 4,
                "fwd_tile": [fplan["family_name"], fplan["waves_per_token"], fplan["chunks_per_lane"],
                             fplan["rows_per_tile"]],
@@ -682,6 +739,8 @@ def batched_sweep(args, results, failed):
 
     dev = torch.device("cuda:0")
     lib, st = _lib.lib(), _lib.stream_ptr(dev)
+    side = torch.cuda.Stream(dev)  # graph captures (device-only times)
+    side_ptr = ctypes.c_void_p(side.cuda_stream)
     P = Workload._p
     dt = getattr(torch, args.dtype)
     code, tag = _lib.dtype_code(dt), DTYPE_TAG[args.dtype]
@@ -706,9 +765,9 @@ def batched_sweep(args, results, failed):
             prev = (n, b, t, d)
         queries = all_queries[:q, :d].contiguous()
 
-        def batched(s, q=q, queries=queries, n=n, nt=nt, d=d):
+        def batched(s, q=q, queries=queries, n=n, nt=nt, d=d, stream=st):
             _lib.check(lib.sy_fwd_batched(P(s["v"]), P(queries), P(s["out"]), n, q, nt, d, nt * d, code, 1e-6,
-                                          st), "sy_fwd_batched")
+                                          stream), "sy_fwd_batched")
 
         for s in sets:  # warm-up: first launches load code objects and query attributes
             batched(s)
@@ -717,6 +776,8 @@ def batched_sweep(args, results, failed):
         iters = 3 if args.quick else 100
         loop = harness.time_loop if args.quick else harness.time_loop_median
         ms = loop([lambda s=s: batched(s) for s in sets], device=dev, iters=iters)
+        gms = None if args.quick else harness.time_graph([lambda s=s: batched(s, stream=side_ptr) for s in sets],
+                                                         stream=side)
         nbytes = attn_res_batched_bytes(n, q, b, t, d, item)
         s0 = sets[0]
         batched(s0)
@@ -732,6 +793,7 @@ def batched_sweep(args, results, failed):
                "impl": "switchyard_hip", "N": n, "B": b, "T": t, "D": d, "Q": q, "dtype": tag,
                "fwd_us": round(ms * 1e3, 2), "fwd_gbps": round(nbytes / ms / 1e6, 1),
                "fwd_frac_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBPS, 4),
+               "fwd_graph_us": None if gms is None else round(gms * 1e3, 2),
                "family": plan["family_name"], "check": check}
         if tag == "bf16":
             rec["reference_rtx_pro_6000_us"] = ref_q_us[q] if config3 else 1e3 * BATCHED_SHAPE_CHECKS[(n, b, t, d)]

@@ -89,3 +89,21 @@ def test_environment_change_warns(tmp_path, capsys):
     _write(tmp_path / "results", "sweep_bf16.json", [_rec()], env=dict(ENV, torch="2.11.0"))
     assert _gate(tmp_path) == 0
     assert "warning: baseline torch='2.10.0'" in capsys.readouterr().out
+
+
+def test_device_only_twins_are_gated_in_place_of_event_times(tmp_path, capsys):
+    """Where both runs carry the graph-replayed (device-only) time, it is
+    gated and the event-timed number (the host's time for tiny shapes) is not;
+    a run without twins falls back to the event-timed numbers."""
+    _write(tmp_path / "results", "sweep_bf16.json", [_rec(fwd=5.0, fb=12.0, fwd_graph_us=3.0, fwd_bwd_graph_us=10.0)])
+    _gate(tmp_path, "--accept")
+    # host jitter: +20% on the event loops, the device times unchanged
+    _write(tmp_path / "results", "sweep_bf16.json", [_rec(fwd=6.0, fb=14.4, fwd_graph_us=3.0, fwd_bwd_graph_us=10.0)])
+    assert _gate(tmp_path) == 0
+    # a device-side slowdown fails
+    _write(tmp_path / "results", "sweep_bf16.json", [_rec(fwd=5.0, fb=12.0, fwd_graph_us=3.0, fwd_bwd_graph_us=11.0)])
+    assert _gate(tmp_path) == 1
+    assert "fwd+bwd us (device)" in capsys.readouterr().out
+    # without twins in the current run the event-timed numbers gate again
+    _write(tmp_path / "results", "sweep_bf16.json", [_rec(fwd=6.0, fb=12.0)])
+    assert _gate(tmp_path) == 1
