@@ -155,8 +155,12 @@ k_batched_mx(const RowTable v, const uint16_t* __restrict__ q, uint16_t* __restr
   // TP tokens per workgroup: waves WV*h .. WV*h + WV-1 own token slot h (its
   // own LDS rows and buffers); the slots of a workgroup advance in step (one
   // barrier per token), so no co-resident slot runs ahead of another.
-  const int half = TP > 1 ? (int)(threadIdx.x / (64 * WV)) : 0;
-  const int w = (threadIdx.x >> 6) % WV;
+  // Both are the same in every lane of a wave; readfirstlane tells the
+  // compiler so. Without it the slot's token index counts as per-lane, and
+  // every buffer load and store built from it is wrapped in a waterfall loop
+  // (readfirstlane, compare, exec mask, branch) that serialises the memory ops.
+  const int half = TP > 1 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x / (64 * WV))) : 0;
+  const int w = __builtin_amdgcn_readfirstlane((int)((threadIdx.x >> 6) % WV));
   char* const vs = vs_all + (size_t)half * (size_t)(n_src + 1) * rs;
   const int qi = lane & 15;  // MFMA column: query (logits, output) / row (A of logits)
   const int g = lane >> 4;   // 16-lane group
