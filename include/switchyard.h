@@ -100,8 +100,11 @@ typedef struct sy_plan {
  * path); a backward without stats may run a thinner tile. The forward and
  * backward launches also take the token count into account: with at most two
  * tokens per CU (16-bit rows of four chunks a lane, 3 <= N <= 16) they run
- * tiles of four or two waves per token, which sy_kernel_info reports and this
- * function, having no token count, does not. Replaces the dispatch helpers _launch_config, _bwd_launch and
+ * tiles of four or two waves per token, and the backward does so also at
+ * N = 2, for fp32 rows, and (up to four tokens per CU) where a wave's row
+ * slice is two chunks a lane; sy_kernel_info and sy_plan_for_tokens report
+ * the launched tile, this function, having no token count, does not.
+ * Replaces the dispatch helpers _launch_config, _bwd_launch and
  * _batched_launch (src/switchyard/triton_op.py:130-150, :267-276, :420-435). */
 int sy_plan_for(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_dtype,
                 int aligned, sy_plan* out);
