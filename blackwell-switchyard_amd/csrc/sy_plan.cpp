@@ -184,6 +184,17 @@ int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_
       }
     }
   }
+  // Rows of 1025-2048 chunks (fp32 D = 8192, 16-bit D = 16384): only eight
+  // waves of four chunks cover them, two waves a SIMD at 256 VGPRs each. The
+  // 4-row tile fits (fp32 167-184 VGPRs, 16-bit 238 with stats, one spilled
+  // without); the 9-row one only for fp32 rows with the forward's stats (4
+  // VGPRs spilled -- 16-bit rows, which keep fp32 copies, spill 92, and the
+  // recompute variants over 100). Elsewhere these rows stay generic.
+  if (vec && op == SY_OP_BWD && e > 64 * 4 * 4 && e <= 64 * 4 * 8 && n_src >= 2 &&
+      (n_src <= 4 || (n_src <= 9 && ce == 4 && has_stats))) {
+    set(out, SY_FAMILY_RESIDENT, 8, 4, n_src <= 4 ? 4 : 9, ce, op, n_src);
+    return SY_OK;
+  }
   if (vec && !(op == SY_OP_BATCHED && n_q > kBatchedMaxQ)) {
     const int budget = op == SY_OP_BWD     ? (has_stats ? kBwdStatsBudget : kBwdBudget)
                        : op == SY_OP_BATCHED ? kBatchedBudget

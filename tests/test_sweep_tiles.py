@@ -121,6 +121,71 @@ def test_32_row_tile_in_fp32(n, t, d):
     assert rel_l2(ww.grad.cpu(), torch.from_numpy(rdw)) <= 1e-5
 
 
+EIGHT_WAVE_CASES = [
+    # rows of 2048 chunks, covered only by eight waves of four chunks: fp32
+    # D=8192 (the d-sweep's B=1 shape, 9 rows; and 4 rows) and 16-bit D=16384
+    ((9, 768, 8192), torch.float32, (8, 4, 9)),
+    ((4, 600, 8192), torch.float32, (8, 4, 4)),
+    ((3, 600, 16384), torch.bfloat16, (8, 4, 4)),
+]
+
+
+@pytest.mark.parametrize("shape,dtype,tile", EIGHT_WAVE_CASES, ids=lambda x: str(x))
+def test_eight_wave_backward_tiles(shape, dtype, tile):
+    """The eight-wave four-chunk backward (two waves a SIMD) against the
+    float64 C oracle: fp32 at the reference's fp32 bars (1e-6 forward, 1e-5
+    gradients), 16-bit at the 1.10x floor."""
+    n, t, d = shape
+    print(f"eight-wave tile N={n} T={t} D={d} {dtype}: expect bwd {tile}", flush=True)
+    assert _tile(_lib.OP_BWD, n, d, dtype, t) == ("resident", tile)
+    if dtype != torch.float32:
+        _check(n, 1, t, d, dtype, seed=7)
+        return
+    gen = torch.Generator().manual_seed(n + d)
+    v = torch.randn(n, 1, t, d, generator=gen)
+    w = 0.5 * torch.randn(d, generator=gen)
+    g = torch.randn(1, t, d, generator=gen)
+    vv, ww = v.to(DEV).requires_grad_(True), w.to(DEV).requires_grad_(True)
+    out = block_attn_res_hip(vv, ww)
+    out.backward(g.to(DEV))
+    v64 = v.double()[:, 0].numpy()
+    ro = torch.from_numpy(c_oracle.forward(v64, w.double().numpy()))
+    rdv, rdw = c_oracle.backward(v64, w.double().numpy(), g.double()[0].numpy())
+    assert rel_l2(out.detach()[0].cpu(), ro) <= 1e-6
+    assert rel_l2(vv.grad[:, 0].cpu(), torch.from_numpy(rdv)) <= 1e-5
+    assert rel_l2(ww.grad.cpu(), torch.from_numpy(rdw)) <= 1e-5
+
+
+def test_fp32_d8192_backward_without_stats_stays_generic():
+    """Without the forward's stats the 9-row eight-wave tile would spill over
+    100 VGPRs, so that call runs the generic kernel, inside the workspace the
+    query sizes (its grid and the tile's), at the fp32 bar."""
+    import ctypes
+
+    n, t, d = 9, 600, 8192
+    gen = torch.Generator().manual_seed(11)
+    v = torch.randn(n, 1, t, d, generator=gen)
+    w = 0.5 * torch.randn(d, generator=gen)
+    g = torch.randn(1, t, d, generator=gen)
+    lib, code = _lib.lib(), _lib.dtype_code(torch.float32)
+    vd, wd, gd = v.to(DEV), w.to(DEV), g.to(DEV)
+    ws_bytes = lib.sy_bwd_workspace_bytes(n, t, d, code, code)
+    assert ws_bytes >= lib.sy_bwd_partial_rows(n, t, d, code, code, 1, 0) * d * 4
+    assert ws_bytes >= lib.sy_bwd_partial_rows(n, t, d, code, code, 1, 1) * d * 4
+    ws = torch.empty(ws_bytes // 4, device=DEV)
+    dv, dw = torch.empty_like(vd), torch.empty(d, device=DEV)
+    P = ctypes.c_void_p
+    rc = lib.sy_bwd(P(vd.data_ptr()), P(wd.data_ptr()), P(gd.data_ptr()), None, P(dv.data_ptr()),
+                    P(dw.data_ptr()), P(ws.data_ptr()), ws_bytes, n, t, d, t * d, code, code, 1e-6,
+                    _lib.stream_ptr(vd.device))
+    assert rc == 0
+    torch.cuda.synchronize()
+    v64 = v.double()[:, 0].numpy()
+    rdv, rdw = c_oracle.backward(v64, w.double().numpy(), g.double()[0].numpy())
+    assert rel_l2(dv[:, 0].cpu(), torch.from_numpy(rdv)) <= 1e-5
+    assert rel_l2(dw.cpu(), torch.from_numpy(rdw)) <= 1e-5
+
+
 def test_32_row_tile_is_bitwise_deterministic_and_other_callers_fall_back():
     """Two runs give the same bits; without the forward's stats the backward
     at N > 16 runs the generic kernel and still matches."""
