@@ -894,6 +894,12 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
     iters = first < n_tok ? (int)((n_tok - first + slots - 1) / slots) : 0;
   }
 
+  // Eight waves of four 16-bit chunks share each SIMD two by two (256 VGPRs a
+  // wave): there w and the token's grad_out stay packed and are widened where
+  // they are used, which frees the 32 VGPRs their fp32 copies would take
+  // beyond the packed ones (at 9 rows the copies spill 92 VGPRs).
+  // (The fp32 copies below are then dead code.)
+  constexpr bool kLean = W == 8 && VPL == 4 && CE == 8;
   float wf[VPL][CE];
   i32x4_t wq[VPL];
   {
@@ -1077,6 +1083,11 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
     for (int j = 0; j < VPL; ++j)
 #pragma unroll
       for (int e = 0; e < CE; ++e) gf[j][e] = elem<T>(gq[j], e);
+    [[maybe_unused]] i32x4_t gk[VPL];  // lean tiles: this token's grad_out, packed
+    if constexpr (kLean) {
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) gk[j] = gq[j];
+    }
     if (more) {
       const auto gr = make_rsrc(g + nxt * d, row_bytes);
 #pragma unroll
@@ -1094,15 +1105,30 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
 #pragma unroll
         for (int j = 0; j < VPL; ++j) {
           float f[CE];
+          if constexpr (kLean) {
+            // Lean tiles widen w and grad_out again for every row: opaque
+            // copies of the packed words keep the compiler from hoisting the
+            // conversions out of the loops, which would rebuild the fp32 copies.
+            i32x4_t wj = wq[j], gj = gk[j];
+            asm volatile("" : "+v"(wj), "+v"(gj));
 #pragma unroll
-          for (int e = 0; e < CE; ++e) {
-            // fp16: an opaque fp32 copy, so that the two FMAs below do not
-            // each fold the conversion into a v_fma_mix (which costs the
-            // tile register moves: N=9 58.2 vs 56.2 us, N=16 103.1 vs 99.1).
-            float xv = elem<T>(x[n][j], e);
-            if constexpr (T::code == F16::code) asm volatile("" : "+v"(xv));
-            f[e] = fmaf(c, xv, fmaf(da, wf[j][e], al[n] * gf[j][e]));
-            dwa[j][e] = fmaf(da_w, xv, dwa[j][e]);
+            for (int e = 0; e < CE; ++e) {
+              float xv = elem<T>(x[n][j], e);
+              if constexpr (T::code == F16::code) asm volatile("" : "+v"(xv));
+              f[e] = fmaf(c, xv, fmaf(da, elem<T>(wj, e), al[n] * elem<T>(gj, e)));
+              dwa[j][e] = fmaf(da_w, xv, dwa[j][e]);
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < CE; ++e) {
+              // fp16: an opaque fp32 copy, so that the two FMAs below do not
+              // each fold the conversion into a v_fma_mix (which costs the
+              // tile register moves: N=9 58.2 vs 56.2 us, N=16 103.1 vs 99.1).
+              float xv = elem<T>(x[n][j], e);
+              if constexpr (T::code == F16::code) asm volatile("" : "+v"(xv));
+              f[e] = fmaf(c, xv, fmaf(da, wf[j][e], al[n] * gf[j][e]));
+              dwa[j][e] = fmaf(da_w, xv, dwa[j][e]);
+            }
           }
           st16_stream(dr, lane_off + j * kStep, pack<T>(f));
         }
@@ -1200,6 +1226,12 @@ k_bwd_tall(const RowTable v, const typename T::storage* __restrict__ w,
   const bool row_lane = lane < rows;
   const int iters = n_iter;  // every slot meets the same barriers
 
+  // Eight waves of four 16-bit chunks share each SIMD two by two (256 VGPRs a
+  // wave): there w and the token's grad_out stay packed and are widened where
+  // they are used, which frees the 32 VGPRs their fp32 copies would take
+  // beyond the packed ones (at 9 rows the copies spill 92 VGPRs).
+  // (The fp32 copies below are then dead code.)
+  constexpr bool kLean = W == 8 && VPL == 4 && CE == 8;
   float wf[VPL][CE];
   i32x4_t wq[VPL];
   {
@@ -1296,6 +1328,11 @@ k_bwd_tall(const RowTable v, const typename T::storage* __restrict__ w,
     for (int j = 0; j < VPL; ++j)
 #pragma unroll
       for (int e = 0; e < CE; ++e) gf[j][e] = elem<T>(gq[j], e);
+    [[maybe_unused]] i32x4_t gk[VPL];  // lean tiles: this token's grad_out, packed
+    if constexpr (kLean) {
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) gk[j] = gq[j];
+    }
     if (more) {
       const auto gr = make_rsrc(g + nxt * d, row_bytes);
 #pragma unroll

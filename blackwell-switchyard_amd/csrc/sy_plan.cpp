@@ -22,6 +22,8 @@
 //     admits 16 rows x 2 chunks when the forward's stats are passed (that
 //     variant holds no recompute state and fits 256 VGPRs); without stats that
 //     tile spills and the thinner one is kept.
+//     Rows of 1025-2048 chunks: eight waves of four chunks, two a SIMD, for
+//     2 <= N <= 4, and up to 9 rows with the forward's stats.
 //     16 < N <= 32 with stats: the 32-row tile, one chunk per lane on the 2 or
 //     4 waves that cover the row, or two chunks on 4 (D = 4096 in bf16).
 //  5. Batched: 16-bit inputs with N <= 16, 4 <= S <= 16 and D in {512, 1024,
@@ -157,8 +159,8 @@ int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_
   // 62.2 vs 64.9 us), and from 2 rows on for 16-bit sources (T=4096 bf16,
   // D=2048: N=2 17.4 vs 18.5 us, N=4 28.5 vs 30.2; D=4096: N=4 52.6 vs 56.1;
   // D=8192: N=4 101.1 vs 109.3). With fp32 sources and N <= 4 two chunks on
-  // twice the waves stay faster (D=2048, N=4: 52.6 vs 58.1 us). Eight waves
-  // of such a tile would share a SIMD and spill. The 16-row tile holds 256 VGPRs of source
+  // twice the waves stay faster (D=2048, N=4: 52.6 vs 58.1 us). Rows of more
+  // than 1024 chunks take eight such waves (below). The 16-row tile holds 256 VGPRs of source
   // rows: its recompute variant (no stats) spills 68 bytes a lane and still
   // beats the thinner tiles (N=16: 119 vs 167 us).
   // 16 < N <= 32 with the forward's stats: 32 rows resident, a token on as
@@ -185,13 +187,15 @@ int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_
     }
   }
   // Rows of 1025-2048 chunks (fp32 D = 8192, 16-bit D = 16384): only eight
-  // waves of four chunks cover them, two waves a SIMD at 256 VGPRs each. The
-  // 4-row tile fits (fp32 167-184 VGPRs, 16-bit 238 with stats, one spilled
-  // without); the 9-row one only for fp32 rows with the forward's stats (4
-  // VGPRs spilled -- 16-bit rows, which keep fp32 copies, spill 92, and the
-  // recompute variants over 100). Elsewhere these rows stay generic.
+  // waves of four chunks cover them, two waves a SIMD at 256 VGPRs each (16-bit
+  // rows keep w and grad_out packed there). The 4-row tile fits (167-225
+  // VGPRs); the 9-row one with the forward's stats spills 4 VGPRs in fp32 and
+  // 51-72 in 16 bits and still runs the backward 4-6x faster than the generic
+  // kernel (bf16 T=2048 D=16384: N=9 313 vs 1842 us, N=5 206 vs 1100; fp32
+  // T=4096 D=8192 N=9 447 vs 1696). Its recompute variants (over 100 spilled)
+  // and more rows stay generic.
   if (vec && op == SY_OP_BWD && e > 64 * 4 * 4 && e <= 64 * 4 * 8 && n_src >= 2 &&
-      (n_src <= 4 || (n_src <= 9 && ce == 4 && has_stats))) {
+      (n_src <= 4 || (n_src <= 9 && has_stats))) {
     set(out, SY_FAMILY_RESIDENT, 8, 4, n_src <= 4 ? 4 : 9, ce, op, n_src);
     return SY_OK;
   }

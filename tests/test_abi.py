@@ -279,9 +279,8 @@ def test_batched_matrix_core_plan_bounds():
 def test_backward_takes_four_chunks_only_with_one_wave_per_simd():
     """Four chunks per lane run one wave per SIMD (256-thread workgroups, 512
     registers, at most 4 waves per token), except on rows of 1025-2048 chunks,
-    which only eight such waves cover (two a SIMD, 256 registers: 4 rows, or 9
-    fp32 rows); every other backward tile runs two waves per SIMD (512
-    threads)."""
+    which only eight such waves cover (two a SIMD, 256 registers; up to 9
+    rows); every other backward tile runs two waves per SIMD (512 threads)."""
     for n in (1, 2, 4, 5, 9, 12, 16):
         for d in (512, 1024, 1536, 2048, 4096, 8192, 16384):
             for dt in (torch.bfloat16, torch.float32):
@@ -290,7 +289,7 @@ def test_backward_takes_four_chunks_only_with_one_wave_per_simd():
                     continue
                 if p["chunks_per_lane"] == 4 and p["waves_per_token"] == 8:
                     assert 1024 < d // (4 if dt == torch.float32 else 8) <= 2048, (n, d, dt, p)
-                    assert 2 <= n <= 4 or (n <= 9 and dt == torch.float32), (n, d, dt, p)
+                    assert 2 <= n <= 9, (n, d, dt, p)
                     assert p["rows_per_tile"] == (4 if n <= 4 else 9), (n, d, dt, p)
                     assert (p["block_threads"], p["tokens_per_block"]) == (512, 1), (n, d, dt, p)
                 elif p["chunks_per_lane"] == 4:
@@ -307,8 +306,9 @@ def test_backward_takes_four_chunks_only_with_one_wave_per_simd():
     assert tile(plan(_lib.OP_BWD, 9, 4096)) == (2, 4, 9)
     assert tile(plan(_lib.OP_BWD, 9, 2048, torch.float32)) == (2, 4, 9)
     assert tile(plan(_lib.OP_BWD, 9, 8192)) == (4, 4, 9)
-    assert tile(plan(_lib.OP_BWD, 9, 16384))[1] <= 2  # eight such waves would share a SIMD and spill
-    assert tile(plan(_lib.OP_BWD, 9, 8192, torch.float32)) == (8, 4, 9)  # fp32 rows: 4 VGPRs spilled
+    assert tile(plan(_lib.OP_BWD, 9, 16384)) == (8, 4, 9)  # two waves a SIMD: spills, still 6x generic
+    assert tile(plan(_lib.OP_BWD, 10, 16384))[1] <= 2
+    assert tile(plan(_lib.OP_BWD, 9, 8192, torch.float32)) == (8, 4, 9)
     assert tile(plan(_lib.OP_BWD, 4, 8192, torch.float32)) == (8, 4, 4)
     assert tile(plan(_lib.OP_BWD, 3, 16384)) == (8, 4, 4)
     assert tile(plan(_lib.OP_BWD, 4, 2048)) == (1, 4, 4)  # few rows, 16-bit: still four chunks

@@ -127,6 +127,9 @@ EIGHT_WAVE_CASES = [
     ((9, 768, 8192), torch.float32, (8, 4, 9)),
     ((4, 600, 8192), torch.float32, (8, 4, 4)),
     ((3, 600, 16384), torch.bfloat16, (8, 4, 4)),
+    # 16-bit rows with 9 rows: w and grad_out kept packed (spills remain)
+    ((9, 560, 16384), torch.bfloat16, (8, 4, 9)),
+    ((6, 600, 16384), torch.float16, (8, 4, 9)),
 ]
 
 
