@@ -68,13 +68,14 @@ __device__ __forceinline__ S* row_at(const RowTable& t, int n) {
 // tiles use 256 threads: one wave per SIMD, so a wave may hold 512 registers
 // (256 VGPRs + 256 AGPRs) -- the 144-register tile plus everything else, with
 // no spills. The 32-row kernel (k_bwd_tall) runs 512 threads with one chunk a
-// lane (two waves per SIMD: a 128-VGPR tile) and 256 with two. Build-time
+// lane (two waves per SIMD: a 128-VGPR tile) and 256 with two; its 64-row
+// tiles (one chunk a lane, 256 tile VGPRs) run 256. Build-time
 // constants so that kernels and the host plan agree.
 #ifndef SY_BWD_BLOCK
 #define SY_BWD_BLOCK 512
 #endif
 constexpr int bwd_block_base(int vpl, int nr) {
-  return nr > 16 ? (vpl == 1 ? 512 : 256) : vpl >= 4 ? 256 : SY_BWD_BLOCK;
+  return nr > 16 ? (vpl == 1 && nr <= 32 ? 512 : 256) : vpl >= 4 ? 256 : SY_BWD_BLOCK;
 }
 constexpr int bwd_block(int w, int vpl, int nr = 0) {
   return bwd_block_base(vpl, nr) > 64 * w ? bwd_block_base(vpl, nr) : 64 * w;

@@ -158,12 +158,12 @@ hipError_t SY_FN(launch_batched_vec_)(const sy_plan& p, const BatchedArgs& a, hi
 // variant: a BwdVariant (kBwdStacked, kBwdListed, kBwdStatsGrad).
 hipError_t SY_FN(bwd_vec_resources_)(const sy_plan& p, bool stats, int variant, KernelRes* out) {
   if (variant < 0 || variant > 2) return hipErrorInvalidValue;
-  // 32-row tiles exist for the stacked operator gradient with stats only.
+  // 32- and 64-row tiles exist for the stacked operator gradient with stats only.
 #define X(W_, V_, N_)                                                                        \
   if (tile_is(p, W_, V_, N_)) {                                                              \
     if (!stats || variant != kBwdStacked) return hipErrorInvalidConfiguration;              \
     static const KernelRes r =                                                               \
-        resources_of(k_bwd_tall<T, W_, V_>, TallGeom<W_, V_>::kBlock);                       \
+        resources_of(k_bwd_tall<T, W_, V_, N_>, TallGeom<W_, V_, N_>::kBlock);               \
     *out = r;                                                                                \
     return hipSuccess;                                                                       \
   }
@@ -195,7 +195,7 @@ hipError_t SY_FN(launch_bwd_vec_)(const sy_plan& p, const BwdArgs& a, int grid, 
 #define X(W_, V_, N_)                                                                        \
   if (tile_is(p, W_, V_, N_)) {                                                              \
     if (a.stats == nullptr || a.listed || a.gm != nullptr) return hipErrorInvalidConfiguration; \
-    hipLaunchKernelGGL((k_bwd_tall<T, W_, V_>), dim3(grid), dim3(TallGeom<W_, V_>::kBlock), 0, \
+    hipLaunchKernelGGL((k_bwd_tall<T, W_, V_, N_>), dim3(grid), dim3(TallGeom<W_, V_, N_>::kBlock), 0, \
                        s, a.v, (const St*)a.w, (const St*)a.g, a.stats, a.dv, a.partial,       \
                        a.n_src, a.n_tok, a.d, inv_d, n_iter);                                 \
     return hipGetLastError();                                                                 \

@@ -1177,34 +1177,36 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
 }
 
 
-// ------------------------------------------------ backward, 17 to 32 sources
+// ------------------------------------------------ backward, 17 to 64 sources
 //
 // The operator's gradient with the forward's stats over stacked rows for
-// 16 < N <= 32: k_bwd's algebra, persistence and row-by-row refill, with the
-// token's per-row scalars laid out across lanes instead of held as uniform
-// values: lane n of one VGPR each carries row n's G_n, logit, r, alpha, da
-// and c. The softmax backward is then a few lane-parallel operations and
-// three wave reductions, where 32 rows of uniform scalar code (as k_bwd
-// writes it) needed ~300 SGPRs and spilled them into VGPR lanes on every
-// token. The dv loop broadcasts row n's three coefficients with readlane as
-// it reaches the row. Rows n >= N are never loaded; their lanes carry
-// logit -inf (weight 0) and zero coefficients.
-template <int W, int VPL>
+// 16 < N <= NR (NR = 32 or 64): k_bwd's algebra, persistence and row-by-row
+// refill, with the token's per-row scalars laid out across lanes instead of
+// held as uniform values: lane n of one VGPR each carries row n's G_n, logit,
+// r, alpha, da and c. The softmax backward is then a few lane-parallel
+// operations and three wave reductions, where 32 rows of uniform scalar code
+// (as k_bwd writes it) needed ~300 SGPRs and spilled them into VGPR lanes on
+// every token. The dv loop broadcasts row n's three coefficients with readlane
+// as it reaches the row. Rows n >= N are never loaded; their lanes carry
+// logit -inf (weight 0) and zero coefficients. 64 rows of one chunk a lane
+// hold 256 tile VGPRs and run one wave per SIMD; their grad dots are summed as
+// two 32-row transposed sums.
+template <int W, int VPL, int NR>
 struct TallGeom {
-  static constexpr int kBlock = bwd_block(W, VPL, 32);
+  static constexpr int kBlock = bwd_block(W, VPL, NR);
   static constexpr int kTpb = kBlock / (64 * W);
 };
 
-template <class T, int W, int VPL>
-__global__ void __launch_bounds__((TallGeom<W, VPL>::kBlock))
+template <class T, int W, int VPL, int NR>
+__global__ void __launch_bounds__((TallGeom<W, VPL, NR>::kBlock))
 k_bwd_tall(const RowTable v, const typename T::storage* __restrict__ w,
            const typename T::storage* __restrict__ g, const float* __restrict__ stats,
            const RowTable dv, float* __restrict__ partial, int n_src, int64_t n_tok, int d,
            float inv_d, int n_iter) {
   using S = typename T::storage;
   constexpr int CE = T::ce;
-  constexpr int NR = 32;
-  constexpr int TPB = TallGeom<W, VPL>::kTpb;
+  static_assert(NR == 32 || NR == 64, "tall tiles hold 32 or 64 rows");
+  constexpr int TPB = TallGeom<W, VPL, NR>::kTpb;
   constexpr uint32_t kStep = 64u * W * 16u;
   constexpr int kLaneFloats = VPL * CE;
   constexpr int kFH = TPB > 1 ? TPB / 2 : 1;
@@ -1222,16 +1224,10 @@ k_bwd_tall(const RowTable v, const typename T::storage* __restrict__ w,
   const uint32_t lane_off = (uint32_t)(seg * 64 + lane) * 16u;
   const int64_t slots = (int64_t)gridDim.x * TPB;
   const int64_t first = (int64_t)blockIdx.x * TPB + slot;
-  const int rows = n_src;  // host guarantees 16 < n_src <= 32
+  const int rows = n_src;  // host guarantees 16 < n_src <= NR
   const bool row_lane = lane < rows;
   const int iters = n_iter;  // every slot meets the same barriers
 
-  // Eight waves of four 16-bit chunks share each SIMD two by two (256 VGPRs a
-  // wave): there w and the token's grad_out stay packed and are widened where
-  // they are used, which frees the 32 VGPRs their fp32 copies would take
-  // beyond the packed ones (at 9 rows the copies spill 92 VGPRs).
-  // (The fp32 copies below are then dead code.)
-  constexpr bool kLean = W == 8 && VPL == 4 && CE == 8;
   float wf[VPL][CE];
   i32x4_t wq[VPL];
   {
@@ -1299,8 +1295,22 @@ k_bwd_tall(const RowTable v, const typename T::storage* __restrict__ w,
           for (int j = 0; j < VPL; ++j) dts[n] = dot<T>(x[n][j], gq[j], dts[n]);
         }
       }
-      const float s = tsum32(dts, lane);
-      if ((lane & 2) == 0) red[k & 1][slot][seg][tsum32_row(lane)] = s;
+      if constexpr (NR == 32) {
+        const float s = tsum32(dts, lane);
+        if ((lane & 2) == 0) red[k & 1][slot][seg][tsum32_row(lane)] = s;
+      } else {
+        float lo[32], hi[32];
+#pragma unroll
+        for (int n = 0; n < 32; ++n) {
+          lo[n] = dts[n];
+          hi[n] = dts[32 + n];
+        }
+        const float s0 = tsum32(lo, lane), s1 = tsum32(hi, lane);
+        if ((lane & 2) == 0) {
+          red[k & 1][slot][seg][tsum32_row(lane)] = s0;
+          red[k & 1][slot][seg][32 + tsum32_row(lane)] = s1;
+        }
+      }
     }
     __syncthreads();
     if (lane < NR) {
@@ -1328,11 +1338,6 @@ k_bwd_tall(const RowTable v, const typename T::storage* __restrict__ w,
     for (int j = 0; j < VPL; ++j)
 #pragma unroll
       for (int e = 0; e < CE; ++e) gf[j][e] = elem<T>(gq[j], e);
-    [[maybe_unused]] i32x4_t gk[VPL];  // lean tiles: this token's grad_out, packed
-    if constexpr (kLean) {
-#pragma unroll
-      for (int j = 0; j < VPL; ++j) gk[j] = gq[j];
-    }
     if (more) {
       const auto gr = make_rsrc(g + nxt * d, row_bytes);
 #pragma unroll

@@ -24,10 +24,14 @@ namespace sy {
 #define SY_BWD_WIDE_TILES(X) X(1, 4, 16) X(2, 4, 16)
 // Backward-only tiles of 32 rows, one or two chunks per lane (128 or 256 tile
 // VGPRs; two waves per SIMD, or one), for 16 < N <= 32 with the forward's stats on stacked rows: the
-// operator's gradient as the autograd op calls it. Other callers at that N
-// (no stats, per-row pointers, the (o, m, l) gradient) run the generic kernel.
-#define SY_BWD_TALL_TILES(X) X(2, 1, 32) X(4, 1, 32) X(2, 2, 32) X(4, 2, 32)
+// operator's gradient as the autograd op calls it; and of 64 rows, one chunk
+// per lane (256 tile VGPRs, one wave per SIMD), for 32 < N <= 64. Other
+// callers at that N (no stats, per-row pointers, the (o, m, l) gradient) run
+// the generic kernel.
+#define SY_BWD_TALL_TILES(X) \
+  X(2, 1, 32) X(4, 1, 32) X(2, 2, 32) X(4, 2, 32) X(2, 1, 64) X(4, 1, 64)
 constexpr int kTallRows = 32;
+constexpr int kTallerRows = 64;
 
 // Largest N the generic kernels accept (their per-token scalars live in LDS).
 constexpr int64_t kGenericMaxN = 4096;

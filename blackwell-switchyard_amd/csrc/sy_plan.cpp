@@ -177,6 +177,14 @@ int make_plan(int op, int64_t n_src, int64_t n_q, int64_t d, int v_dtype, int w_
       return SY_OK;
     }
   }
+  // 32 < N <= 64 with stats: 64 rows of one chunk a lane on two or four waves
+  // (rows of up to 256 chunks: 16-bit D <= 2048, fp32 D <= 1024), one wave per
+  // SIMD.
+  if (vec && op == SY_OP_BWD && has_stats && n_src > kTallRows && n_src <= kTallerRows && e > 64 &&
+      e <= 256) {
+    set(out, SY_FAMILY_RESIDENT, e <= 128 ? 2 : 4, 1, kTallerRows, ce, op, n_src);
+    return SY_OK;
+  }
   if (vec && op == SY_OP_BWD && (n_src > 4 || (n_src >= 2 && ce == 8)) && n_src <= 16) {
     for (int ww : {1, 2, 4}) {
       if (n_src > 9 && ww == 4) break;

@@ -232,8 +232,16 @@ def test_large_n_forward_uses_online_chunks_and_backward_the_32_row_tile():
         assert p["family_name"] == "resident", (n, d)
         assert (p["waves_per_token"], p["chunks_per_lane"], p["rows_per_tile"]) == tile
         assert p["block_threads"] == (512 if tile[1] == 1 else 256)  # two waves per SIMD, or one
-    # beyond 32 rows, above 4096 bf16 columns or below 128: generic
-    for n, d in ((33, 2048), (32, 8192), (20, 512)):
+    # 32 < N <= 64: 64 rows of one chunk a lane on two or four waves, one wave
+    # per SIMD (rows of at most 256 chunks)
+    for n, d, dt, tile in ((33, 2048, torch.bfloat16, (4, 1, 64)), (64, 1024, torch.float16, (2, 1, 64)),
+                           (48, 1024, torch.float32, (4, 1, 64)), (40, 512, torch.float32, (2, 1, 64))):
+        p = plan(_lib.OP_BWD, n, d, dt)
+        assert (p["family_name"], p["waves_per_token"], p["chunks_per_lane"], p["rows_per_tile"]) == \
+            ("resident",) + tile, (n, d, dt)
+        assert p["block_threads"] == 256
+    # beyond 64 rows, above 4096 bf16 columns (2048 past 32 rows) or below 128: generic
+    for n, d in ((65, 2048), (32, 8192), (33, 4096), (20, 512), (40, 512)):
         assert plan(_lib.OP_BWD, n, d)["family_name"] == "generic", (n, d)
 
 

@@ -121,6 +121,46 @@ def test_32_row_tile_in_fp32(n, t, d):
     assert rel_l2(ww.grad.cpu(), torch.from_numpy(rdw)) <= 1e-5
 
 
+TALLER_CASES = [
+    # 32 < N <= 64: the 64-row backward tile (a per-layer AttnRes model's
+    # readout sees n_blocks + 1 sources), in each dtype, partly filled at N=33
+    ((33, 600, 2048), torch.bfloat16, (4, 1, 64)),
+    ((64, 300, 1024), torch.float16, (2, 1, 64)),
+    ((48, 256, 1024), torch.float32, (4, 1, 64)),
+]
+
+
+@pytest.mark.parametrize("shape,dtype,tile", TALLER_CASES, ids=lambda x: str(x))
+def test_64_row_backward_tile(shape, dtype, tile):
+    """The 64-row tile against the float64 C oracle (16-bit at the 1.10x floor,
+    fp32 at 1e-6 / 1e-5), and bit for bit the same on a second run."""
+    n, t, d = shape
+    print(f"64-row tile N={n} T={t} D={d} {dtype}: expect bwd {tile}", flush=True)
+    assert _tile(_lib.OP_BWD, n, d, dtype, t) == ("resident", tile)
+    gen = torch.Generator().manual_seed(n + t)
+    v = torch.randn(n, 1, t, d, generator=gen).to(dtype)
+    w = (0.5 * torch.randn(d, generator=gen)).to(dtype)
+    g = torch.randn(1, t, d, generator=gen).to(dtype)
+    runs = []
+    for _ in range(2):
+        vv, ww = v.to(DEV).requires_grad_(True), w.to(DEV).requires_grad_(True)
+        out = block_attn_res_hip(vv, ww)
+        out.backward(g.to(DEV))
+        runs.append((out.detach().cpu(), vv.grad.cpu(), ww.grad.cpu()))
+    for a, b in zip(runs[0], runs[1]):
+        assert torch.equal(a, b)
+    out, dv, dw = runs[0]
+    v64 = v.double()[:, 0].numpy()
+    ro = torch.from_numpy(c_oracle.forward(v64, w.double().numpy()))
+    rdv, rdw = c_oracle.backward(v64, w.double().numpy(), g.double()[0].numpy())
+    for name, got, ref, bar in (("out", out[0], ro, 1e-6), ("dv", dv[:, 0], torch.from_numpy(rdv), 1e-5),
+                                ("dw", dw, torch.from_numpy(rdw), 1e-5)):
+        err = rel_l2(got, ref)
+        if dtype != torch.float32:
+            bar = 1.10 * dtype_floor(ref, dtype)
+        assert err <= bar, f"{name}: rel_l2 {err:.4e} vs {bar:.4e}"
+
+
 EIGHT_WAVE_CASES = [
     # rows of 2048 chunks, covered only by eight waves of four chunks: fp32
     # D=8192 (the d-sweep's B=1 shape, 9 rows; and 4 rows) and 16-bit D=16384
