@@ -25,7 +25,9 @@
 //     Rows of 1025-2048 chunks: eight waves of four chunks, two a SIMD, for
 //     2 <= N <= 4, and up to 9 rows with the forward's stats.
 //     16 < N <= 32 with stats: the 32-row tile, one chunk per lane on the 2 or
-//     4 waves that cover the row, or two chunks on 4 (D = 4096 in bf16).
+//     4 waves that cover the row, or two chunks on 4 (D = 4096 in bf16);
+//     32 < N <= 64 with stats: the 64-row tile, one chunk per lane on 2 or 4
+//     waves (rows of up to 256 chunks).
 //  5. Batched: 16-bit inputs with N <= 16, 4 <= S <= 16 and D in {512, 1024,
 //     1536, 2048} run on the matrix cores (config 3: 8 queries x 9 rows is ~7000
 //     VALU instructions a token on the register tile); otherwise resident with
