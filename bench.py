@@ -85,9 +85,11 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--quick", action="store_true",
                     help="--schedule / --sweep: a few launches per row and a copy-probe calibration "
                          "launch at the end (a rocprofv3 --pmc target)")
-    ap.add_argument("--traffic-set", default="config2", choices=["config2", "schedule", "n32", "n4", "n16"],
+    ap.add_argument("--traffic-set", default="config2",
+                    choices=["config2", "schedule", "n32", "n4", "n16", "d8192f32"],
                     help="--traffic: which kernels and workload the counter runs covered (nN: "
-                         "bench.py --sweep --sweep-only NN --quick)")
+                         "bench.py --sweep --sweep-only NN --quick; d8192f32: bench.py --sweep "
+                         "--dtype float32 --sweep-only d-sweep-b1 --quick)")
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--sweep-only", default=None,
                     help="comma list of sweep names (n-sweep, t-sweep, d-sweep, d-sweep-b1, batch, small, "
@@ -469,6 +471,13 @@ def _traffic_kernels(args):
         wl = f"N={n} B=1 T=4096 D={d} bf16"
         fwd = ("fwd", "k_fwd_res", None) if n <= 9 else ("fwd_chunked", "k_fwd<", None)
         return [(*fwd, (n + 1) * slab, wl), ("bwd_main", "k_bwd<", None, (2 * n + 1) * slab, wl)]
+    if args.traffic_set == "d8192f32":  # bench.py --sweep --dtype float32 --sweep-only d-sweep-b1 --quick
+        n, d = 9, 8192
+        slab = 4096 * d * 4
+        wl = f"N={n} B=1 T=4096 D={d} fp32"
+        # the eight-wave tiles run only at D=8192 in that set
+        return [("fwd", "k_fwd_res<sy::F32, 8, 4, 9", None, (n + 1) * slab, wl),
+                ("bwd_main", "k_bwd<sy::F32, 8, 4, 9, true, 0>", None, (2 * n + 1) * slab, wl)]
     n, d = 32, 2048  # bench.py --sweep --sweep-only N32 --quick
     slab = 4096 * d * 2
     wl = f"N={n} B=1 T=4096 D={d} bf16"

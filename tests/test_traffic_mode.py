@@ -83,6 +83,25 @@ def test_n_sweep_sets_match_their_kernels(tmp_path, traffic_set, n, fwd_name, fw
     assert rec["bwd_main_algorithmic_bytes"] == (2 * n + 1) * SLAB
 
 
+def test_fp32_d8192_set_matches_the_eight_wave_tiles(tmp_path):
+    """The d-sweep's fp32 counter run holds every D of the set: only the
+    eight-wave kernels of D=8192 count, at fp32 slabs."""
+    gib_kib = float(1 << 20)
+    fwd8 = "void sy::k_fwd_res<sy::F32, 8, 4, 9, false, false>(x)"
+    bwd8 = "void sy::k_bwd<sy::F32, 8, 4, 9, true, 0>(x)"
+    other = [("void sy::k_fwd_res<sy::F32, 4, 4, 9, false, false>(x)", 999.0),
+             ("void sy::k_bwd<sy::F32, 4, 4, 9, true, 0>(x)", 999.0)]
+    fetch = [(PROBE, gib_kib / 2), (fwd8, 10.0), (bwd8, 20.0), *other]
+    write = [(PROBE, gib_kib), (fwd8, 1.0), (bwd8, 2.0), *other]
+    rec = _run(tmp_path, fetch, write, "d8192f32")
+    slab = 4096 * 8192 * 4
+    assert rec["workload"] == "N=9 B=1 T=4096 D=8192 fp32"
+    assert rec["fwd_bytes_per_launch"] == round((10.0 * 2 + 1.0) * 1024)
+    assert rec["bwd_main_bytes_per_launch"] == round((20.0 * 2 + 2.0) * 1024)
+    assert rec["fwd_algorithmic_bytes"] == 10 * slab
+    assert rec["bwd_main_algorithmic_bytes"] == 19 * slab
+
+
 def test_a_missing_kernel_is_an_error(tmp_path):
     gib_kib = float(1 << 20)
     fetch = [(PROBE, gib_kib / 2)]
