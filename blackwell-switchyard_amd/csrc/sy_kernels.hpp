@@ -900,6 +900,12 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
   // beyond the packed ones (at 9 rows the copies spill 92 VGPRs).
   // (The fp32 copies below are then dead code.)
   constexpr bool kLean = W == 8 && VPL == 4 && CE == 8;
+  // dv store policy: nt plus the device-scope bit for 16-bit 9-row tiles whose
+  // wave slice spans four chunks (MI355X, backward main kernel, bf16 T=4096, two
+  // interleaved rounds: D=2048 55.5 -> 55.1 us, D=4096 110.4 -> 109.3, D=8192
+  // 223.2 -> 221.5), nt alone elsewhere (N=4 27.6 vs 28.8, N=16 97.4 vs 98.2,
+  // fp32 N=9 111.8 vs 112.7, D=1024 B=4 (two chunks) 118.9 vs 119.5 with the bit).
+  constexpr int kDvAux = CE == 8 && NR == 9 && W * VPL >= 4 ? SY_DV_STORE_AUX : SY_STREAM_STORE_AUX;
   float wf[VPL][CE];
   i32x4_t wq[VPL];
   {
@@ -1130,7 +1136,7 @@ k_bwd(const RowTable v, const typename T::storage* __restrict__ w,
               dwa[j][e] = fmaf(da_w, xv, dwa[j][e]);
             }
           }
-          st16_stream(dr, lane_off + j * kStep, pack<T>(f));
+          st16_aux<kDvAux>(dr, lane_off + j * kStep, pack<T>(f));
         }
         if (more) {
           const auto r = make_rsrc(row_at<LISTED, const S>(v, n) + nxt * d, row_bytes);
@@ -1373,7 +1379,9 @@ k_bwd_tall(const RowTable v, const typename T::storage* __restrict__ w,
             f[e] = fmaf(cn, xv, fmaf(dan, wf[j][e], aln * gf[j][e]));
             dwa[j][e] = fmaf(da_w, xv, dwa[j][e]);
           }
-          st16_stream(dr, lane_off + j * kStep, pack<T>(f));
+          // nt plus the device-scope bit (bf16 backward N=32 207.1 -> 201.6 us, N=48
+          // 352.7 -> 348.4)
+          st16_aux<SY_DV_STORE_AUX>(dr, lane_off + j * kStep, pack<T>(f));
         }
         if (more) {
           const auto r = make_rsrc(vrow, row_bytes);
