@@ -112,9 +112,10 @@ __device__ __forceinline__ void st16(__amdgpu_buffer_rsrc_t r, uint32_t off, i32
 __device__ __forceinline__ void st16_stream(__amdgpu_buffer_rsrc_t r, uint32_t off, i32x4_t x) {
   __builtin_amdgcn_raw_buffer_store_b128(x, r, off, 0, SY_STREAM_STORE_AUX);
 }
-// dv stores of the operator backward's 16-bit 9-row tiles and of its 32- and
-// 64-row tiles also carry the device-scope bit (sc1 = 16) next to nt; the other
-// tiles measured slower with it (see the backward kernels).
+// Policy of the dv stores that measured faster with the device-scope bit (sc1 = 16)
+// next to nt: the operator backward's 16-bit 9-row tiles whose wave slice spans four
+// chunks, and its 32- and 64-row tiles (k_bwd, k_bwd_tall); the other tiles and
+// kernels measured slower with it and keep SY_STREAM_STORE_AUX.
 #ifndef SY_DV_STORE_AUX
 #define SY_DV_STORE_AUX 18
 #endif
