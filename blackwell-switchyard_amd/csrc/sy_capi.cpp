@@ -495,7 +495,7 @@ int sy_attn_with_stats_merge(const void* v, const void* w, const void* o1, const
   sy_plan p;
   rc = make_plan(SY_OP_FWD, n_src + 1, 0, d, v_dtype, w_dtype, aligned, &p);
   if (rc != SY_OK) return rc;
-  apply_tile_rules(SY_OP_FWD, n_src + 1, n_tok, d, &p);
+  apply_tile_rules(SY_OP_FWD, n_src + 1, n_tok, d, &p, /*chunked_ok=*/false);
   if (n_tok == 0) return SY_OK;
   if (p.family == SY_FAMILY_RESIDENT && n_src + 1 <= kTableRows && p.rows_per_tile >= n_src + 1) {
     t.p[n_src] = const_cast<void*>(o1);

@@ -200,10 +200,12 @@ bool tuning_snapshot(sy_tuning* out);
 // never applies it.
 void apply_tile_override(int op, int64_t n_src, int64_t d, sy_plan* p);
 // The plan's tile for n_tok tokens: the token-count rule (wider tiles when
-// there are at most two tokens per CU, forward and backward), then any
-// sy_tuning_set tile override. Every launch and size query of the forward and
-// backward applies it, so grids and workspaces agree.
-void apply_tile_rules(int op, int64_t n_src, int64_t n_tok, int64_t d, sy_plan* p);
+// there are few tokens per CU, forward and backward), then any sy_tuning_set
+// tile override. Every launch and size query of the forward and backward
+// applies it, so grids and workspaces agree. `chunked_ok` false keeps the
+// forward over 10-16 rows resident (callers that need a resident tile).
+void apply_tile_rules(int op, int64_t n_src, int64_t n_tok, int64_t d, sy_plan* p,
+                      bool chunked_ok = true);
 
 // Launches the matrix-core batched forward (a.n_src etc. must pass
 // matrix_batched_fits). With `info` != nullptr fills it and launches nothing.

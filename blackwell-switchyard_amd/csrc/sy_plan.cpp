@@ -311,7 +311,17 @@ void apply_tile_override(int op, int64_t n_src, int64_t d, sy_plan* p) {
 // 4% either way, so the plan's tile); D = 512 (two chunks) N=9 T=256
 // 8.92 -> 7.25, T=1024 10.70 -> 9.33. The fp32 forward was not measured and
 // keeps its tiles.
-void apply_token_rule(int op, int64_t n_src, int64_t n_tok, sy_plan* p) {
+// The forward over 10-16 rows (16-bit D = 2048, the chunked family) keeps its
+// four-row chunks and spreads a token over four waves up to three tokens per
+// CU, over two up to six (HIP-graph replays, bf16, us, plan tile -> this rule):
+//   N=16 T=256 10.60 -> 10.12, T=512 14.09 -> 12.13, T=768 15.18 -> 14.17,
+//        T=1024 17.24 -> 16.23, T=1280 22.58 -> 17.97, T=1536 23.36 -> 20.16
+//   N=12 T=512 11.95 -> 9.87, T=1024 13.98 -> 13.08; N=10 T=256 8.38 -> 7.60
+// (fp16 the same within 0.2 us); at eight tokens per CU the one-wave chunks
+// stay (N=16 T=2048: 26.1 vs 28.1 us on two waves). Where a caller needs a
+// resident tile (the fused merge carries its prior as one more row),
+// `chunked_ok` false keeps the 16-row resident tiles of the rule below.
+void apply_token_rule(int op, int64_t n_src, int64_t n_tok, sy_plan* p, bool chunked_ok) {
   if (op != SY_OP_FWD && op != SY_OP_BWD) return;
   const bool tiled = p->family == SY_FAMILY_RESIDENT || p->family == SY_FAMILY_CHUNKED;
   const bool bwd = op == SY_OP_BWD;
@@ -321,7 +331,15 @@ void apply_token_rule(int op, int64_t n_src, int64_t n_tok, sy_plan* p) {
   if (span != 4 && !(span == 2 && bwd && p->waves_per_token == 1)) return;
   int cus = 0;
   if (cu_count(&cus) != hipSuccess || cus < 1) return;
-  if (n_tok < 1 || n_tok > (span == 4 ? 2 : 4) * (int64_t)cus) return;
+  if (n_tok < 1) return;
+  if (!bwd && n_src > 9 && chunked_ok) {
+    if (n_tok > 6 * (int64_t)cus) return;
+    const int wc = n_tok <= 3 * (int64_t)cus ? 4 : 2;
+    if (!tile_listed(op, wc, 4 / wc, 4)) return;
+    set(p, SY_FAMILY_CHUNKED, wc, 4 / wc, 4, p->elems_per_chunk, op, n_src);
+    return;
+  }
+  if (n_tok > (span == 4 ? 2 : 4) * (int64_t)cus) return;
   const int nr = n_src <= 4 ? 4 : n_src <= 9 ? 9 : 16;
   const int w = span == 2 ? (n_tok <= 2 * (int64_t)cus ? 4 : 2) : (bwd || n_tok <= cus ? 4 : 2);
   const int vpl = span == 2 ? 1 : 4 / w;
@@ -329,8 +347,8 @@ void apply_token_rule(int op, int64_t n_src, int64_t n_tok, sy_plan* p) {
   set(p, SY_FAMILY_RESIDENT, w, vpl, nr, p->elems_per_chunk, op, n_src);
 }
 
-void apply_tile_rules(int op, int64_t n_src, int64_t n_tok, int64_t d, sy_plan* p) {
-  apply_token_rule(op, n_src, n_tok, p);
+void apply_tile_rules(int op, int64_t n_src, int64_t n_tok, int64_t d, sy_plan* p, bool chunked_ok) {
+  apply_token_rule(op, n_src, n_tok, p, chunked_ok);
   apply_tile_override(op, n_src, d, p);
 }
 

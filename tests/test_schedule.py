@@ -242,6 +242,29 @@ def test_fused_phase_two_against_the_oracle(case, dtype, normalize):
     _stat_close(ell[0].cpu(), rl, "l")
 
 
+def test_fused_phase_two_keeps_its_resident_tile_at_small_token_counts():
+    """At two tokens per CU the forward over 13 rows runs four-row chunks, but
+    the fused phase 2 carries its prior as a 13th row and keeps the resident
+    16-row tile: one rounding (the 1.10x bar), where the two-kernel fallback
+    would round twice."""
+    from switchyard.stats_op import attn_with_stats_merge
+
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    n, t, d, dtype = 12, 2 * cus, 2048, torch.bfloat16
+    assert _lib.plan(_lib.OP_FWD, n + 1, d, dtype, n_tok=t)["family_name"] == "chunked"
+    v, w = _make(n, t, d, dtype, seed=5)
+    g = torch.Generator().manual_seed(6)
+    o1 = torch.randn(1, t, d, generator=g).to(dtype).to(DEV)
+    m1 = torch.randn(1, t, generator=g).to(DEV)
+    l1 = (1.0 + 3.0 * torch.rand(1, t, generator=g)).to(DEV)
+    out, m, ell = attn_with_stats_merge(v, w, o1, m1, l1, normalize=True)
+    ro2, rm2, rl2 = c_oracle.attn_with_stats(_np(v)[:, 0], _np(w))
+    ro, rm, rl = c_oracle.merge(_np(o1)[0], _np(m1)[0], _np(l1)[0], ro2, rm2, rl2)
+    _close(out[0].cpu(), ro / rl[:, None], dtype, mult=1.10, what="out")
+    _stat_close(m[0].cpu(), rm, "m")
+    _stat_close(ell[0].cpu(), rl, "l")
+
+
 def test_fused_phase_two_chains_and_matches_the_three_kernel_composition():
     """Three groups: phase 2 unnormalised, then again normalised, equals the
     operator over all sources; and the fused two-phase output sits within one

@@ -72,7 +72,8 @@ SWEEP_CASES = [
     ((4, 1, 768, 8192), ("resident", (4, 4, 4)), (4, 4, 4)),
     ((9, 1, 768, 8192), ("resident", (4, 4, 9)), (4, 4, 9)),
     # N between the sweep points: the 16-row backward with a partly filled tile
-    ((12, 1, 4 * 256, 2048), ("chunked", (1, 4, 4)), (1, 4, 16)),
+    # (four tokens per CU: the forward's four-row chunks on two waves)
+    ((12, 1, 4 * 256, 2048), ("chunked", (2, 2, 4)), (1, 4, 16)),
     # D sweep tiles (config 4 uses B=4 T=4096; the tile depends only on the
     # token count being above two per CU, four for the D=1024 backward)
     ((9, 4, 512, 1024), ("resident", (1, 2, 9)), (1, 2, 9)),

@@ -1,6 +1,8 @@
 """The token-count tile rule (GPU). At D = 2048 with at most two tokens per CU
 the forward runs (4,1,NR) up to one token per CU and (2,2,NR) up to two
-(N >= 3), the backward (4,1,NR) (N >= 2). Where a wave's row slice is two
+(3 <= N <= 9), the backward (4,1,NR) (N >= 2); the forward over 10-16 rows
+keeps four-row chunks on four waves up to three tokens per CU and on two up
+to six. Where a wave's row slice is two
 chunks a lane (16-bit D = 1024, fp32 D = 512) the backward runs (4,1,NR) up to
 two tokens per CU and (2,1,NR) up to four; fp32 rows of four chunks
 (D = 1024) take the backward's (4,1,NR) up to two tokens per CU. Above that
@@ -45,7 +47,11 @@ def _run(n, t, d, seed, dtype=torch.bfloat16):
     (9, 2, 2048, "2,2,9", "4,1,9", torch.bfloat16),
     (9, 2, 2048, "2,2,9", "4,1,9", torch.float16),
     (4, 2, 2048, "2,2,4", "4,1,4", torch.bfloat16),
-    (16, 2, 2048, "2,2,16", "4,1,16", torch.bfloat16),
+    (16, 2, 2048, "4,1,4", "4,1,16", torch.bfloat16),
+    (12, 3, 2048, "4,1,4", "1,4,16", torch.float16),
+    (16, 5, 2048, "2,2,4", "1,4,16", torch.bfloat16),
+    (10, 6, 2048, "2,2,4", "1,4,16", torch.bfloat16),
+    (16, 8, 2048, "1,4,4", "1,4,16", torch.bfloat16),
     (9, 4, 2048, "1,4,9", "1,4,9", torch.bfloat16),
     (2, 1, 2048, "1,4,4", "4,1,4", torch.bfloat16),
     (2, 4, 2048, "1,4,4", "1,4,4", torch.bfloat16),
