@@ -102,7 +102,9 @@ typedef struct sy_plan {
  * tokens per CU (16-bit rows of four chunks a lane, 3 <= N <= 16) they run
  * tiles of four or two waves per token, and the backward does so also at
  * N = 2, for fp32 rows, and (up to four tokens per CU) where a wave's row
- * slice is two chunks a lane; sy_kernel_info and sy_plan_for_tokens report
+ * slice is two chunks a lane; the forward over 10-16 rows keeps four-row
+ * chunks on four waves up to three tokens per CU and on two up to six;
+ * sy_kernel_info and sy_plan_for_tokens report
  * the launched tile, this function, having no token count, does not.
  * Replaces the dispatch helpers _launch_config, _bwd_launch and
  * _batched_launch (src/switchyard/triton_op.py:130-150, :267-276, :420-435). */
