@@ -309,8 +309,8 @@ void apply_tile_override(int op, int64_t n_src, int64_t d, sy_plan* p) {
 // (four chunks a lane) N=9 T=128 9.75 -> 7.52, T=512 11.24 -> 9.19, N=16
 // T=128 16.65 -> 12.67, N=4 T=256 5.81 -> 4.49 (four tokens per CU: within
 // 4% either way, so the plan's tile); D = 512 (two chunks) N=9 T=256
-// 8.92 -> 7.25, T=1024 10.70 -> 9.33. The fp32 forward was not measured and
-// keeps its tiles.
+// 8.92 -> 7.25, T=1024 10.70 -> 9.33. The fp32 forward has a branch of its own
+// (below).
 // The forward over 10-16 rows (16-bit D = 2048, the chunked family) keeps its
 // four-row chunks and spreads a token over four waves up to three tokens per
 // CU, over two up to six (HIP-graph replays, bf16, us, plan tile -> this rule):
@@ -326,8 +326,29 @@ void apply_token_rule(int op, int64_t n_src, int64_t n_tok, sy_plan* p, bool chu
   const bool tiled = p->family == SY_FAMILY_RESIDENT || p->family == SY_FAMILY_CHUNKED;
   const bool bwd = op == SY_OP_BWD;
   if (!tiled || n_src < 2 || n_src > 16) return;
-  if (!bwd && (p->elems_per_chunk != 8 || n_src < 3)) return;  // forward: 16-bit rows, N >= 3
   const int span = p->waves_per_token * p->chunks_per_lane;  // one wave's chunks a lane
+  if (!bwd && p->elems_per_chunk == 4) {
+    // fp32 forward: four waves a token up to one token per CU (rows of four or
+    // eight chunks a lane), and for 10-16 rows four-row chunks on four waves up
+    // to two (HIP-graph replays, us, plan tile -> this rule: N=9 D=2048 T=256
+    // 8.65 -> 7.59, D=1024 6.94 -> 5.99; N=16 D=2048 T=512 18.25 -> 16.18; at
+    // two tokens per CU the 9-row plan tiles stay, 10.63 vs 10.90, and from four
+    // tokens per CU every plan tile).
+    if (n_src < 3 || (span != 4 && span != 8)) return;
+    int cus = 0;
+    if (cu_count(&cus) != hipSuccess || cus < 1 || n_tok < 1) return;
+    const int vv = span / 4;
+    if (n_src > 9) {
+      if (!chunked_ok || n_tok > 2 * (int64_t)cus || !tile_listed(op, 4, vv, 4)) return;
+      set(p, SY_FAMILY_CHUNKED, 4, vv, 4, p->elems_per_chunk, op, n_src);
+      return;
+    }
+    const int nr4 = n_src <= 4 ? 4 : 9;
+    if (n_tok > cus || !tile_listed(op, 4, vv, nr4)) return;
+    set(p, SY_FAMILY_RESIDENT, 4, vv, nr4, p->elems_per_chunk, op, n_src);
+    return;
+  }
+  if (!bwd && (p->elems_per_chunk != 8 || n_src < 3)) return;  // forward: 16-bit rows, N >= 3
   if (span != 4 && !(span == 2 && bwd && p->waves_per_token == 1)) return;
   int cus = 0;
   if (cu_count(&cus) != hipSuccess || cus < 1) return;

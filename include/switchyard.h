@@ -103,7 +103,9 @@ typedef struct sy_plan {
  * tiles of four or two waves per token, and the backward does so also at
  * N = 2, for fp32 rows, and (up to four tokens per CU) where a wave's row
  * slice is two chunks a lane; the forward over 10-16 rows keeps four-row
- * chunks on four waves up to three tokens per CU and on two up to six;
+ * chunks on four waves up to three tokens per CU and on two up to six, and
+ * fp32 forwards take four waves a token up to one token per CU (10-16 rows:
+ * two);
  * sy_kernel_info and sy_plan_for_tokens report
  * the launched tile, this function, having no token count, does not.
  * Replaces the dispatch helpers _launch_config, _bwd_launch and
