@@ -349,6 +349,21 @@ void apply_token_rule(int op, int64_t n_src, int64_t n_tok, sy_plan* p, bool chu
     return;
   }
   if (!bwd && (p->elems_per_chunk != 8 || n_src < 3)) return;  // forward: 16-bit rows, N >= 3
+  if (span == 8 && p->elems_per_chunk == 8 && n_src <= 9) {
+    // 16-bit rows of eight chunks a lane (D = 4096) up to one token per CU: the
+    // forward on four waves of two chunks, the backward on eight of one (HIP-graph
+    // replays, bf16, us, plan tile -> this rule: N=9 T=256 forward 9.50 -> 7.88,
+    // backward 12.40 -> 10.56; T=128 8.80 -> 6.77, 11.51 -> 8.55; N=4 T=256
+    // 5.40 -> 4.47, 7.26 -> 6.29; at two tokens per CU the plan tiles stay,
+    // 11.53 vs 11.99 and 15.8 vs 16.4).
+    int cus8 = 0;
+    if (cu_count(&cus8) != hipSuccess || cus8 < 1 || n_tok < 1 || n_tok > cus8) return;
+    const int nr8 = n_src <= 4 ? 4 : 9;
+    const int w8 = bwd ? 8 : 4, v8 = bwd ? 1 : 2;
+    if (!tile_listed(op, w8, v8, nr8)) return;
+    set(p, SY_FAMILY_RESIDENT, w8, v8, nr8, p->elems_per_chunk, op, n_src);
+    return;
+  }
   if (span != 4 && !(span == 2 && bwd && p->waves_per_token == 1)) return;
   int cus = 0;
   if (cu_count(&cus) != hipSuccess || cus < 1) return;

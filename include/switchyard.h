@@ -105,7 +105,8 @@ typedef struct sy_plan {
  * slice is two chunks a lane; the forward over 10-16 rows keeps four-row
  * chunks on four waves up to three tokens per CU and on two up to six, and
  * fp32 forwards take four waves a token up to one token per CU (10-16 rows:
- * two);
+ * two), and 16-bit D = 4096 up to one token per CU runs the forward on four
+ * waves and the backward on eight;
  * sy_kernel_info and sy_plan_for_tokens report
  * the launched tile, this function, having no token count, does not.
  * Replaces the dispatch helpers _launch_config, _bwd_launch and

@@ -3,7 +3,8 @@ the forward runs (4,1,NR) up to one token per CU and (2,2,NR) up to two
 (3 <= N <= 9), the backward (4,1,NR) (N >= 2); the forward over 10-16 rows
 keeps four-row chunks on four waves up to three tokens per CU and on two up
 to six. fp32 forwards take four waves a token up to one token per CU (10-16
-rows: four-row chunks up to two). Where a wave's row slice is two
+rows: four-row chunks up to two); 16-bit D = 4096 up to one token per CU runs
+the forward on four waves of two chunks and the backward on eight of one. Where a wave's row slice is two
 chunks a lane (16-bit D = 1024, fp32 D = 512) the backward runs (4,1,NR) up to
 two tokens per CU and (2,1,NR) up to four; fp32 rows of four chunks
 (D = 1024) take the backward's (4,1,NR) up to two tokens per CU. Above that
@@ -63,6 +64,9 @@ def _run(n, t, d, seed, dtype=torch.bfloat16):
     (9, 4, 1024, "1,2,9", "2,1,9", torch.bfloat16),
     (4, 4, 1024, "1,2,4", "2,1,4", torch.bfloat16),
     (9, 8, 1024, "1,2,9", "1,2,9", torch.bfloat16),
+    (9, 1, 4096, "4,2,9", "8,1,9", torch.bfloat16),
+    (4, 1, 4096, "4,2,4", "8,1,4", torch.float16),
+    (9, 2, 4096, "2,4,9", "2,4,9", torch.bfloat16),
     (9, 1, 1024, "4,1,9", "4,1,9", torch.float32),
     (9, 1, 2048, "4,2,9", "2,4,9", torch.float32),
     (9, 2, 2048, "2,4,9", "2,4,9", torch.float32),
